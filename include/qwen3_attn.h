@@ -1,0 +1,205 @@
+/*
+ * qwen3_attn.h — C ABI of the MI355X (gfx950) attention hot path of the
+ * Qwen3 inference engine: paged decode attention, varlen causal prefill
+ * attention, and the paged KV-cache slot writes.
+ *
+ * Conventions shared by every entry point
+ *   - All pointers are device pointers (HBM) unless stated otherwise; the
+ *     library never allocates, frees or synchronises.  Work is enqueued on
+ *     `stream` (a hipStream_t passed as void*; NULL = the null stream), so a
+ *     caller inside stream capture records the launches into its graph.
+ *   - Tensors are bf16 (raw 16-bit storage).  Strides are in ELEMENTS, not
+ *     bytes; the innermost (head_dim) stride is always 1.
+ *   - Indices into the resident tables are int32, as the reference keeps them.
+ *   - Every entry point returns 0 on success, a negative QWEN3_E* code when an
+ *     argument is rejected before anything is launched, or the positive
+ *     hipError_t of a failed launch.  qwen3_attn_last_error() returns a
+ *     human-readable message for the calling thread's last failure.
+ *   - Out-of-range page ids, row ids and slots read from device tables are
+ *     skipped by the kernels (never dereferenced), so a corrupt table cannot
+ *     make a kernel read or write outside the buffers it was given.
+ *
+ * Reference interfaces replaced (file:line in uphome/Qwen3-engine-from-scratch)
+ *   qwen3_paged_decode_bf16    <- paged_attention_decode_triton
+ *                                 (qwen3/kernels/paged_attention.py:132-178)
+ *                                 + paged_attn_decode_kernel (:27-129)
+ *   qwen3_kv_write_decode_bf16 <- update_kv_batch_triton
+ *                                 (qwen3/kernels/paged_attention.py:353-377)
+ *                                 + update_kv_batch_kernel (:292-350)
+ *   qwen3_kv_write_range_bf16  <- PagedKVCache.update advanced-indexing write
+ *                                 (qwen3/PagedKVcache.py:177-214)
+ *   qwen3_kv_write_slots_bf16  <- the per-request B-loop of PagedKVCache.update
+ *                                 in batched prefill (qwen3/attention.py:160-161)
+ *                                 collapsed into one slot-mapped launch
+ *   qwen3_varlen_prefill_bf16  <- flash_attention_prefill
+ *                                 (qwen3/kernels/flash_attention_varlen.py:126-194)
+ *                                 + flash_attention_varlen_kernel (:25-123)
+ */
+#ifndef QWEN3_ATTN_H
+#define QWEN3_ATTN_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define QWEN3_OK 0
+#define QWEN3_EINVAL (-1)       /* bad shape / size / stride / null pointer */
+#define QWEN3_EALIGN (-2)       /* pointer or stride breaks required alignment */
+#define QWEN3_EUNSUPPORTED (-3) /* head_dim / block_size / group size not built */
+#define QWEN3_EWORKSPACE (-4)   /* workspace missing or too small */
+
+/* Message for the calling thread's last failed call ("" if none). */
+const char* qwen3_attn_last_error(void);
+
+/* ABI version of this library (bumped on any signature change). */
+int qwen3_attn_abi_version(void);
+
+/* ------------------------------------------------------------------------
+ * Paged decode attention (GQA), one query token per sequence.
+ *
+ * Replaces paged_attention_decode_triton
+ * (qwen3/kernels/paged_attention.py:132-178): for each batch entry b,
+ *   row = row_ids ? row_ids[b] : b
+ *   L   = seq_lens[row] + seq_len_bias      (the reference passes bias = 1:
+ *                                            seq_lens holds the pre-step
+ *                                            length, :55)
+ *   out[b, h, :] = softmax(scale * q[b, h, :] . K[0:L]^T) V[0:L]
+ * where token t of the sequence lives in physical page
+ * block_table[row * bt_row_stride + t / block_size] at slot t % block_size,
+ * and query head h reads KV head h / (num_heads / num_kv_heads).
+ *
+ *   q          (B, num_heads, head_dim)     strides q_strides[0..1]
+ *   k_cache    per-layer view (num_blocks, num_kv_heads, block_size, head_dim)
+ *              strides k_strides[0..2] (the layer stride is folded into
+ *              k_strides[0], as the reference's pool.k_buffer[:, layer] view)
+ *   v_cache    same layout, strides v_strides[0..2]
+ *   out        (B, num_heads, head_dim)     strides out_strides[0..1]
+ *   block_table int32 (max_rows, max_pages), row stride bt_row_stride
+ *   seq_lens   int32 (max_rows,)
+ *   row_ids    int32 (B,) or NULL (identity)
+ *   workspace  device scratch of at least qwen3_paged_decode_workspace_bytes()
+ *              bytes (split-KV partials); its size depends only on
+ *              (B, num_heads, head_dim, max_pages, block_size), never on the
+ *              live lengths, so one launch shape serves a captured graph.
+ * Supported: head_dim 128, block_size a multiple of 16,
+ *            num_heads / num_kv_heads in [1, 16].
+ * ---------------------------------------------------------------------- */
+size_t qwen3_paged_decode_workspace_bytes(int B, int num_heads, int head_dim,
+                                          int64_t max_pages, int block_size);
+
+int qwen3_paged_decode_bf16(const void* q, const int64_t q_strides[2],
+                            const void* k_cache, const int64_t k_strides[3],
+                            const void* v_cache, const int64_t v_strides[3],
+                            int64_t num_blocks,
+                            const int32_t* block_table, int64_t bt_row_stride,
+                            int64_t max_rows, int64_t max_pages,
+                            const int32_t* seq_lens, int seq_len_bias,
+                            const int32_t* row_ids,
+                            void* out, const int64_t out_strides[2],
+                            int B, int num_heads, int num_kv_heads, int head_dim,
+                            int block_size, float scale,
+                            void* workspace, size_t workspace_bytes,
+                            void* stream);
+
+/* ------------------------------------------------------------------------
+ * Decode-form K/V slot write.
+ *
+ * Replaces update_kv_batch_triton (qwen3/kernels/paged_attention.py:353-377):
+ * for each (b, h):
+ *   row  = row_ids[b];  pos = seq_lens[row]
+ *   phys = block_table[row * bt_row_stride + pos / block_size]
+ *   k_cache[phys, layer_idx, h, pos % block_size, :] = k_new[b, h, :]
+ *   v_cache[...same...]                              = v_new[b, h, :]
+ *   k_new, v_new  (B, num_kv_heads, head_dim), strides *_new_strides[0..1]
+ *                 (non-contiguous slices of a fused QKV output are fine)
+ *   k_cache/v_cache  full pool (num_blocks, num_layers, num_kv_heads,
+ *                 block_size, head_dim), strides *_cache_strides[0..3]
+ * The copy is bit-exact.
+ * ---------------------------------------------------------------------- */
+int qwen3_kv_write_decode_bf16(const void* k_new, const int64_t k_new_strides[2],
+                               const void* v_new, const int64_t v_new_strides[2],
+                               void* k_cache, const int64_t k_cache_strides[4],
+                               void* v_cache, const int64_t v_cache_strides[4],
+                               int64_t num_blocks, int layer_idx,
+                               const int32_t* seq_lens,
+                               const int32_t* block_table, int64_t bt_row_stride,
+                               int64_t max_rows, int64_t max_pages,
+                               const int32_t* row_ids,
+                               int B, int num_kv_heads, int head_dim,
+                               int block_size, void* stream);
+
+/* ------------------------------------------------------------------------
+ * Range-form K/V slot write for one sequence (prefill of one request).
+ *
+ * Replaces the advanced-indexing write of PagedKVCache.update
+ * (qwen3/PagedKVcache.py:197-214): for s in [0, num_tokens), h:
+ *   pos  = start_pos + s
+ *   phys = block_table_row[pos / block_size]
+ *   k_cache[phys, layer_idx, h, pos % block_size, :] = k_new[s, h, :]
+ *   k_new, v_new  (num_tokens, num_kv_heads, head_dim), strides
+ *                 *_new_strides[0] (token) and [1] (head); the reference's
+ *                 (1, Hkv, S, D) tensor passes its S stride as [0], its
+ *                 head stride as [1]
+ *   block_table_row  int32 (row_pages,) — one row of the resident table
+ * ---------------------------------------------------------------------- */
+int qwen3_kv_write_range_bf16(const void* k_new, const int64_t k_new_strides[2],
+                              const void* v_new, const int64_t v_new_strides[2],
+                              void* k_cache, const int64_t k_cache_strides[4],
+                              void* v_cache, const int64_t v_cache_strides[4],
+                              int64_t num_blocks, int layer_idx,
+                              const int32_t* block_table_row, int64_t row_pages,
+                              int64_t start_pos, int64_t num_tokens,
+                              int num_kv_heads, int head_dim, int block_size,
+                              void* stream);
+
+/* ------------------------------------------------------------------------
+ * Slot-mapped K/V write (batched prefill).
+ *
+ * For t in [0, num_tokens), h:  slot = slot_mapping[t];
+ *   if slot < 0 the token is skipped (padding), otherwise
+ *   k_cache[slot / block_size, layer_idx, h, slot % block_size, :] = k_new[t, h, :]
+ * slot_mapping is int64 (num_tokens,).  Equivalent, per request, to the
+ * write of PagedKVCache.update (qwen3/PagedKVcache.py:197-214) with
+ * slot = phys * block_size + offset.
+ * ---------------------------------------------------------------------- */
+int qwen3_kv_write_slots_bf16(const void* k_new, const int64_t k_new_strides[2],
+                              const void* v_new, const int64_t v_new_strides[2],
+                              void* k_cache, const int64_t k_cache_strides[4],
+                              void* v_cache, const int64_t v_cache_strides[4],
+                              int64_t num_blocks, int layer_idx,
+                              const int64_t* slot_mapping, int64_t num_tokens,
+                              int num_kv_heads, int head_dim, int block_size,
+                              void* stream);
+
+/* ------------------------------------------------------------------------
+ * Varlen flash-attention prefill (packed sequences, GQA, causal).
+ *
+ * Replaces flash_attention_prefill
+ * (qwen3/kernels/flash_attention_varlen.py:126-194): sequence s occupies
+ * packed rows [cu_seqlens[s], cu_seqlens[s+1]); query row i of a sequence
+ * attends keys j <= i of the same sequence (all j when causal == 0);
+ * query head h reads KV head h / (num_heads / num_kv_heads).
+ *   q, o      (total_tokens, num_heads, head_dim),    strides *_strides[0..1]
+ *   k, v      (total_tokens, num_kv_heads, head_dim), strides *_strides[0..1]
+ *   cu_seqlens int32 (num_seqs + 1,) on the device
+ *   max_seqlen host-side upper bound of the sequence lengths (sizes the grid;
+ *             the reference syncs cu_seqlens to the host to get it, :177-178)
+ * Supported: head_dim 128, num_heads / num_kv_heads in [1, 16].
+ * ---------------------------------------------------------------------- */
+int qwen3_varlen_prefill_bf16(const void* q, const int64_t q_strides[2],
+                              const void* k, const int64_t k_strides[2],
+                              const void* v, const int64_t v_strides[2],
+                              void* o, const int64_t o_strides[2],
+                              const int32_t* cu_seqlens, int num_seqs,
+                              int max_seqlen, int64_t total_tokens,
+                              int num_heads, int num_kv_heads, int head_dim,
+                              float scale, int causal, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* QWEN3_ATTN_H */

@@ -1,0 +1,117 @@
+"""The C-ABI library loads, exports every function include/qwen3_attn.h
+declares, and rejects bad arguments before launching anything.  CPU only: no
+call here reaches a kernel launch."""
+import ctypes
+import re
+from pathlib import Path
+
+import pytest
+import torch
+
+from qwen3_engine_from_scratch_amd import _lib
+
+HEADER = Path(__file__).resolve().parent.parent / "include" / "qwen3_attn.h"
+
+
+def declared_functions():
+    text = HEADER.read_text()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(qwen3_[a-z0-9_]+)\s*\(", text)))
+
+
+def test_header_declares_the_abi():
+    names = declared_functions()
+    assert "qwen3_paged_decode_bf16" in names and "qwen3_varlen_prefill_bf16" in names
+    assert sorted(names) == sorted(_lib.exported_symbols())
+
+
+def test_library_exports_every_declared_symbol():
+    lib = _lib.load()
+    for name in declared_functions():
+        assert hasattr(lib, name), name
+    assert lib.qwen3_attn_abi_version() == _lib.ABI_VERSION
+
+
+def test_workspace_bytes():
+    lib = _lib.load()
+    # 256 batch x 32 heads x ceil(512 pages * 16 / 256) partitions x (128 + 1) fp32
+    parts = -(-512 * 16 // 256)
+    slots = 256 * 32 * parts
+    expect = -(-slots * 128 * 4 // 256) * 256 + -(-slots * 4 // 256) * 256
+    assert lib.qwen3_paged_decode_workspace_bytes(256, 32, 128, 512, 16) == expect
+    assert lib.qwen3_paged_decode_workspace_bytes(4, 16, 64, 64, 16) == 0  # head_dim 64 not built
+    assert lib.qwen3_paged_decode_workspace_bytes(4, 16, 128, 64, 8) == 0  # block_size 8
+
+
+def _s(*v):
+    return (ctypes.c_int64 * len(v))(*v)
+
+
+FAKE = 1 << 20  # a 16-byte aligned non-null address; never dereferenced on these paths
+
+
+def test_decode_rejects_bad_arguments():
+    lib = _lib.load()
+    args = dict(q=FAKE, qs=_s(4096, 128), k=FAKE, ks=_s(65536, 2048, 128), v=FAKE,
+                vs=_s(65536, 2048, 128), nb=64, bt=FAKE, bts=8, rows=4, mp=8, sl=FAKE, bias=1,
+                rid=None, out=FAKE, os=_s(4096, 128), B=2, H=32, Hk=8, D=128, bs=16,
+                scale=0.088, ws=FAKE, wsb=1 << 30, stream=None)
+
+    def call(**over):
+        a = dict(args, **over)
+        return lib.qwen3_paged_decode_bf16(
+            a["q"], a["qs"], a["k"], a["ks"], a["v"], a["vs"], a["nb"], a["bt"], a["bts"],
+            a["rows"], a["mp"], a["sl"], a["bias"], a["rid"], a["out"], a["os"], a["B"], a["H"],
+            a["Hk"], a["D"], a["bs"], a["scale"], a["ws"], a["wsb"], a["stream"])
+
+    assert call(D=64) == -3
+    assert call(bs=8) == -3
+    assert call(H=30) == -3            # not a multiple of Hkv
+    assert call(H=8 * 17) == -3        # group of 17 > 16
+    assert call(q=None) == -1
+    assert call(bts=4) == -1           # row stride shorter than the row
+    assert call(q=FAKE + 2) == -2      # misaligned
+    assert call(qs=_s(4097, 128)) == -2
+    assert call(ws=None, mp=64, bts=64) == -4  # several partitions need the workspace
+    assert "workspace" in lib.qwen3_attn_last_error().decode()
+
+
+def test_prefill_rejects_bad_arguments():
+    lib = _lib.load()
+    s2 = _s(2048, 128)
+
+    def call(D=128, H=16, Hk=8, q=FAKE, qs=s2):
+        return lib.qwen3_varlen_prefill_bf16(q, qs, FAKE, _s(1024, 128), FAKE, _s(1024, 128), FAKE, s2,
+                                             FAKE, 2, 100, 150, H, Hk, D, 0.088, 1, None)
+
+    assert call(D=256) == -3
+    assert call(H=12, Hk=8) == -3
+    assert call(q=None) == -1
+    assert call(qs=_s(2048, 129)) == -2
+
+
+def test_kv_write_rejects_bad_arguments():
+    lib = _lib.load()
+    c4 = _s(1 << 16, 1 << 14, 2048, 128)
+    rc = lib.qwen3_kv_write_range_bf16(FAKE, _s(1024, 128), FAKE, _s(1024, 128), FAKE, c4, FAKE, c4,
+                                       64, 0, FAKE, 2, 20, 40, 8, 128, 16, None)
+    assert rc == -1  # positions 20..59 need 4 pages, the row has 2
+    rc = lib.qwen3_kv_write_decode_bf16(FAKE, _s(1024, 128), FAKE, _s(1024, 128), FAKE, c4, FAKE, c4,
+                                        64, 0, None, FAKE, 8, 4, 8, None, 2, 8, 128, 16, None)
+    assert rc == -1  # null seq_lens
+
+
+def test_wrappers_refuse_cpu_tensors():
+    """No CPU fallback: the product path raises instead of computing on the host."""
+    from qwen3_engine_from_scratch_amd.kernels.paged_attention import paged_attention_decode_hip
+    from qwen3_engine_from_scratch_amd.kernels.flash_attention_varlen import flash_attention_prefill
+
+    q = torch.zeros(2, 16, 128, dtype=torch.bfloat16)
+    kb = torch.zeros(8, 8, 16, 128, dtype=torch.bfloat16)
+    bt = torch.zeros(2, 4, dtype=torch.int32)
+    sl = torch.zeros(2, dtype=torch.int32)
+    with pytest.raises(RuntimeError, match="no CPU fallback"):
+        paged_attention_decode_hip(q, kb, kb, bt, sl, None, 16)
+    cu = torch.tensor([0, 2], dtype=torch.int32)
+    with pytest.raises(RuntimeError, match="no CPU fallback"):
+        flash_attention_prefill(q, q[:, :8], q[:, :8], cu, 0.088, 16, 8, 128, max_seqlen=2)

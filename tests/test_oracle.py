@@ -1,0 +1,290 @@
+"""Pins the CPU oracle against what the mathematics fixes (closed forms,
+invariants, special cases), and shows that plausible mistakes fail those
+checks.  CPU only."""
+import numpy as np
+import pytest
+import torch
+import torch.nn.functional as F
+
+from oracle import decode as od
+from oracle import inputs as oi
+from oracle import kv_write as ok
+from oracle import prefill as op
+
+DECODE_CASES = [
+    # lens, Hq, Hkv, block_size, seed
+    ([1, 2, 15, 16, 17], 4, 4, 16, 1),
+    ([37, 128, 50], 16, 8, 16, 2),
+    ([5, 33, 64, 100], 8, 2, 16, 3),
+    ([31, 32, 65], 8, 2, 32, 4),
+]
+
+
+def _oracle(case, **kw):
+    return od.paged_attention_ref(case.q, case.k_pool, case.v_pool, case.block_table,
+                                  case.seq_lens, case.row_ids, case.block_size, **kw)
+
+
+def _dense(case, **kw):
+    return od.dense_decode_ref(case.q, case.k_pool, case.v_pool, case.block_table,
+                               case.seq_lens, case.row_ids, case.block_size, **kw)
+
+
+@pytest.mark.parametrize("lens,hq,hkv,bs,seed", DECODE_CASES)
+def test_decode_oracle_matches_fp64_closed_form(lens, hq, hkv, bs, seed):
+    case = oi.make_decode_case(lens, hq, hkv, 128, bs, slack=0.5, seed=seed)
+    got = _oracle(case, out_fp32=True).double()
+    ref = _dense(case)
+    assert (got - ref).abs().max().item() < 2e-5
+
+
+def test_decode_oracle_single_token_returns_v0():
+    case = oi.make_decode_case([1, 1, 1], 8, 2, 128, 16, slack=1.0, seed=5)
+    out = _oracle(case)
+    for b in range(3):
+        phys = int(case.block_table[b, 0])
+        for h in range(8):
+            assert torch.equal(out[b, h], case.v_pool[phys, h // 4, 0])
+
+
+def test_decode_oracle_constant_keys_give_mean_value():
+    case = oi.make_decode_case([40, 77], 4, 2, 128, 16, seed=6)
+    case.k_pool[:] = case.k_pool[0, 0, 0]
+    out = _oracle(case, out_fp32=True).double()
+    for b, L in enumerate(case.lens):
+        vc = od.gather_context(case.v_pool, case.block_table[b], L, 16).double()
+        for h in range(4):
+            assert torch.allclose(out[b, h], vc[h // 2].mean(0), atol=1e-5)
+
+
+def test_decode_oracle_gqa_head_map():
+    # V of KV head j is the constant j+1: query head h must read (h // G) + 1.
+    case = oi.make_decode_case([20, 45], 8, 2, 128, 16, seed=7)
+    for j in range(2):
+        case.v_pool[:, j] = float(j + 1)
+    out = _oracle(case, out_fp32=True)
+    for h in range(8):
+        assert torch.allclose(out[:, h], torch.full_like(out[:, h], float(h // 4 + 1)))
+
+
+def test_decode_oracle_page_permutation_is_bit_identical():
+    case = oi.make_decode_case([70, 33], 8, 4, 128, 16, slack=0.5, seed=8)
+    base = _oracle(case)
+    g = torch.Generator().manual_seed(99)
+    perm = torch.randperm(case.k_pool.shape[0], generator=g)
+    inv = torch.empty_like(perm)
+    inv[perm] = torch.arange(perm.numel())
+    case.k_pool = case.k_pool[perm].clone()
+    case.v_pool = case.v_pool[perm].clone()
+    bt = case.block_table.clone()
+    m = bt >= 0
+    bt[m] = inv[bt[m].long()].to(torch.int32)
+    case.block_table = bt
+    assert torch.equal(_oracle(case), base)
+
+
+def test_decode_oracle_ignores_tail_slots():
+    case = oi.make_decode_case([19, 50], 4, 2, 128, 16, seed=9)
+    base = _oracle(case)
+    for b, L in enumerate(case.lens):
+        last = int(case.block_table[b, (L - 1) // 16])
+        case.k_pool[last, :, L % 16 or 16:] = 1e4
+        case.v_pool[last, :, L % 16 or 16:] = -1e4
+    assert torch.equal(_oracle(case), base)
+
+
+def test_decode_closed_form_check_rejects_planted_mistakes():
+    """Each plausible slip makes the oracle disagree with the closed form."""
+    case = oi.make_decode_case([37, 64, 90], 8, 2, 128, 16, slack=0.5, seed=10)
+    ref = _dense(case)
+
+    def err(x):
+        return (x.double() - ref).abs().max().item()
+
+    assert err(_oracle(case, out_fp32=True)) < 2e-5
+    # dropped "+1" of L = seq_lens + 1
+    assert err(_oracle(case, out_fp32=True, bias=0)) > 1e-3
+    # wrong softmax scale
+    assert err(_oracle(case, out_fp32=True, scale=1.0)) > 1e-3
+    # wrong GQA map (h % Hkv instead of h // G): permute query heads accordingly
+    G, Hkv = 4, 2
+    src = [(h % Hkv) * G + (h // Hkv) for h in range(8)]
+    bad = case.q.clone()
+    bad[:, src] = case.q
+    mut = od.paged_attention_ref(bad, case.k_pool, case.v_pool, case.block_table,
+                                 case.seq_lens, case.row_ids, 16, out_fp32=True)
+    assert err(mut[:, src]) > 1e-3
+    # pages walked in the wrong order
+    rev = case.block_table.clone()
+    for b, L in enumerate(case.lens):
+        n = (L + 15) // 16
+        rev[b, :n] = case.block_table[b, :n].flip(0)
+    mut = od.paged_attention_ref(case.q, case.k_pool, case.v_pool, rev, case.seq_lens,
+                                 case.row_ids, 16, out_fp32=True)
+    assert err(mut) > 1e-3
+
+
+# ---------------------------------------------------------------- prefill
+PREFILL_CASES = [([1, 7, 64, 100], 4, 2, 0), ([33, 129], 8, 8, 1), ([200], 16, 8, 2)]
+
+
+@pytest.mark.parametrize("lens,hq,hkv,seed", PREFILL_CASES)
+def test_varlen_ref_matches_sdpa(lens, hq, hkv, seed):
+    c = oi.make_prefill_case(lens, hq, hkv, 128, seed=seed)
+    got = op.varlen_attention_ref(c.q, c.k, c.v, c.cu_seqlens, c.scale).double()
+    G = hq // hkv
+    for s in range(len(lens)):
+        s0, s1 = int(c.cu_seqlens[s]), int(c.cu_seqlens[s + 1])
+        qs = c.q[s0:s1].double().transpose(0, 1)[None]
+        ks = c.k[s0:s1].double().transpose(0, 1).repeat_interleave(G, 0)[None]
+        vs = c.v[s0:s1].double().transpose(0, 1).repeat_interleave(G, 0)[None]
+        ref = F.scaled_dot_product_attention(qs, ks, vs, is_causal=True, scale=c.scale)
+        assert (got[s0:s1] - ref[0].transpose(0, 1)).abs().max().item() < 2e-5
+
+
+def test_varlen_ref_single_token_and_packing_order():
+    c = oi.make_prefill_case([1, 9, 1, 30], 4, 2, 128, seed=3)
+    out = op.varlen_attention_ref(c.q, c.k, c.v, c.cu_seqlens, c.scale)
+    for s in (0, 2):
+        t = int(c.cu_seqlens[s])
+        for h in range(4):
+            assert torch.equal(out[t, h], c.v[t, h // 2].float())
+    # reverse the sequence order of the pack: per-sequence outputs unchanged
+    segs = [(int(c.cu_seqlens[s]), int(c.cu_seqlens[s + 1])) for s in range(4)][::-1]
+    idx = torch.cat([torch.arange(a, b) for a, b in segs])
+    cu2 = torch.zeros(5, dtype=torch.int32)
+    cu2[1:] = torch.cumsum(torch.tensor([b - a for a, b in segs], dtype=torch.int32), 0)
+    out2 = op.varlen_attention_ref(c.q[idx], c.k[idx], c.v[idx], cu2, c.scale)
+    assert torch.allclose(out2, out[idx], atol=1e-6)
+
+
+def test_varlen_ref_rejects_planted_mistakes():
+    c = oi.make_prefill_case([50, 80], 4, 2, 128, seed=4)
+    ref = op.varlen_attention_ref(c.q, c.k, c.v, c.cu_seqlens, c.scale)
+    noncausal = op.varlen_attention_ref(c.q, c.k, c.v, c.cu_seqlens, c.scale, causal=False)
+    assert (noncausal - ref).abs().max().item() > 1e-2
+    swapped = op.varlen_attention_ref(c.q, c.v, c.k, c.cu_seqlens, c.scale)
+    assert (swapped - ref).abs().max().item() > 1e-2
+
+
+def test_flash_restatement_within_bf16_of_closed_form():
+    c = oi.make_prefill_case([1, 40, 95], 4, 2, 128, seed=5)
+    got = op.flash_varlen_ref(c.q, c.k, c.v, c.cu_seqlens, c.scale).double()
+    ref = op.varlen_attention_ref(c.q, c.k, c.v, c.cu_seqlens, c.scale, dtype=torch.float64)
+    d = (got - ref).abs()
+    assert d.max().item() < 2e-2 and d.mean().item() < 2e-3
+
+
+def test_standard_attention_restatement_on_padded_batch():
+    lens = [5, 48, 31]
+    S = 48
+    c = oi.make_prefill_case(lens, 4, 2, 128, seed=6)
+    qp = op.pad_batch(c.q, c.cu_seqlens, S)
+    kp = op.pad_batch(c.k, c.cu_seqlens, S)
+    vp = op.pad_batch(c.v, c.cu_seqlens, S)
+    mask = op.prefill_mask(lens, S)
+    out = op.standard_attention_ref(qp, kp, vp, mask, c.scale).view(3, S, 4, 128)
+    ref = op.varlen_attention_ref(c.q, c.k, c.v, c.cu_seqlens, c.scale, dtype=torch.float64)
+    for b, L in enumerate(lens):
+        s0 = int(c.cu_seqlens[b])
+        d = (out[b, :L].double() - ref[s0:s0 + L]).abs()
+        assert d.max().item() < 5e-2 and d.mean().item() < 5e-3
+        for h in range(4):  # pad rows see column 0 only
+            for s in range(L, S):
+                assert torch.equal(out[b, s, h], vp[b, h // 2, 0])
+
+
+def test_prefill_mask_pattern():
+    m = op.prefill_mask([2, 3], 3, dtype=torch.float32)[:, 0]
+    inf = float("-inf")
+    exp0 = torch.tensor([[0, inf, inf], [0, 0, inf], [0, inf, inf]])
+    exp1 = torch.tensor([[0, inf, inf], [0, 0, inf], [0, 0, 0]])
+    assert torch.equal(m[0], exp0) and torch.equal(m[1], exp1)
+
+
+# ---------------------------------------------------------------- KV writes
+def _pool(nb=12, layers=3, hkv=2, bs=16, d=128):
+    return np.zeros((nb, layers, hkv, bs, d), np.uint16), np.zeros((nb, layers, hkv, bs, d), np.uint16)
+
+
+def test_kv_write_round_trip_through_block_table():
+    rng = np.random.default_rng(0)
+    kb, vb = _pool()
+    table = np.full((3, 4), -1, np.int32)
+    perm = rng.permutation(12)
+    lens = [20, 33, 7]
+    layer = 1
+    written = {}
+    off = 0
+    for r, L in enumerate(lens):
+        n = (L + 1 + 15) // 16  # room for one decode token
+        table[r, :n] = perm[off:off + n]
+        off += n
+        k_new = rng.integers(0, 2 ** 16, (L, 2, 128), dtype=np.uint16)
+        v_new = rng.integers(0, 2 ** 16, (L, 2, 128), dtype=np.uint16)
+        ok.paged_update_ref(k_new, v_new, kb, vb, table[r], 0, layer)
+        written[r] = [k_new, v_new]
+    # one decode token per request at position L (rows in shuffled order)
+    row_ids = np.array([2, 0, 1], np.int32)
+    seq_lens = np.array(lens, np.int32)
+    kd = rng.integers(0, 2 ** 16, (3, 2, 128), dtype=np.uint16)
+    vd = rng.integers(0, 2 ** 16, (3, 2, 128), dtype=np.uint16)
+    ok.update_kv_batch_ref(kd, vd, kb, vb, seq_lens, table, row_ids, layer)
+    for b, r in enumerate(row_ids):
+        written[r][0] = np.concatenate([written[r][0], kd[b:b + 1]])
+        written[r][1] = np.concatenate([written[r][1], vd[b:b + 1]])
+    touched = np.zeros(kb.shape, bool)
+    for r, L in enumerate(lens):
+        gk = ok.gather_tokens(kb, layer, table[r], L + 1)
+        gv = ok.gather_tokens(vb, layer, table[r], L + 1)
+        assert np.array_equal(gk, written[r][0].transpose(1, 0, 2))
+        assert np.array_equal(gv, written[r][1].transpose(1, 0, 2))
+        for p in range(L + 1):
+            touched[table[r, p // 16], layer, :, p % 16] = True
+    assert not kb[~touched].any() and not vb[~touched].any()
+
+
+def test_kv_write_round_trip_rejects_planted_mistake():
+    """Swapping page and offset in the slot formula breaks the round trip."""
+    rng = np.random.default_rng(1)
+    kb, vb = _pool()
+    table = rng.permutation(12)[:3].astype(np.int32)
+    k_new = rng.integers(1, 2 ** 16, (40, 2, 128), dtype=np.uint16)
+    pos = np.arange(40)
+    bad = np.zeros_like(kb)
+    bad[table[pos % 3], 0, :, pos // 3] = k_new  # wrong: page from pos % n_pages
+    assert not np.array_equal(ok.gather_tokens(bad, 0, table, 40), k_new.transpose(1, 0, 2))
+    ok.paged_update_ref(k_new, k_new, kb, vb, table, 0, 0)
+    assert np.array_equal(ok.gather_tokens(kb, 0, table, 40), k_new.transpose(1, 0, 2))
+
+
+def test_kv_write_numpy_matches_reference_torch_indexing():
+    """The reference statement k_buffer[phys, layer, :, off] = k_new[0].permute(1, 0, 2)
+    (qwen3/PagedKVcache.py:213) run in torch equals the numpy restatement."""
+    rng = np.random.default_rng(2)
+    kb, vb = _pool()
+    table = rng.permutation(12)[:4].astype(np.int32)
+    start, S = 9, 30
+    k_new = rng.integers(0, 2 ** 16, (S, 2, 128), dtype=np.uint16)
+    ok.paged_update_ref(k_new, k_new, kb, vb, table, start, 2)
+    tb = torch.zeros(kb.shape, dtype=torch.int32)
+    pos = torch.arange(start, start + S)
+    phys = torch.from_numpy(table.astype(np.int64))[pos // 16]
+    kt = torch.from_numpy(k_new.astype(np.int32)).unsqueeze(0).permute(0, 2, 1, 3)  # (1,Hkv,S,D)
+    tb[phys, 2, :, pos % 16] = kt[0].permute(1, 0, 2)
+    assert np.array_equal(tb.numpy().astype(np.uint16), kb)
+
+
+def test_slots_form_equals_range_form():
+    rng = np.random.default_rng(3)
+    ka, va = _pool()
+    kb2, vb2 = _pool()
+    table = rng.permutation(12)[:5].astype(np.int32)
+    k_new = rng.integers(0, 2 ** 16, (70, 2, 128), dtype=np.uint16)
+    ok.paged_update_ref(k_new, k_new, ka, va, table, 3, 0)
+    pos = np.arange(3, 73)
+    slots = table[pos // 16].astype(np.int64) * 16 + pos % 16
+    slots_pad = np.concatenate([slots, -np.ones(5, np.int64)])
+    k_pad = np.concatenate([k_new, rng.integers(0, 2 ** 16, (5, 2, 128), dtype=np.uint16)])
+    ok.slots_write_ref(k_pad, k_pad, kb2, vb2, slots_pad, 0)
+    assert np.array_equal(ka, kb2)

@@ -1,0 +1,95 @@
+"""Varlen prefill kernel vs the oracle / fp32 references on the GPU."""
+import pytest
+import torch
+
+from conftest import announce
+from gpu_helpers import assert_close_attn
+from oracle import inputs as oi
+from oracle import prefill as op
+
+pytestmark = pytest.mark.gpu
+
+
+def _run(c, dev, hq, hkv, causal=True):
+    from qwen3_engine_from_scratch_amd.kernels.flash_attention_varlen import flash_attention_prefill
+
+    out = flash_attention_prefill(c.q.to(dev), c.k.to(dev), c.v.to(dev), c.cu_seqlens.to(dev),
+                                  c.scale, hq, hkv, 128, max_seqlen=max(c.lens), causal=causal)
+    torch.cuda.synchronize()
+    return out.cpu()
+
+
+@pytest.mark.parametrize("lens,hq,hkv", [
+    ([1, 7, 64, 100], 16, 8),
+    ([33, 129, 2], 8, 8),        # G = 1
+    ([200, 65], 32, 8),          # G = 4
+    ([150], 16, 2),              # G = 8
+    ([96, 31], 40, 8),           # G = 5
+])
+def test_prefill_small_vs_closed_form(gpu, lens, hq, hkv):
+    c = oi.make_prefill_case(lens, hq, hkv, 128, seed=len(lens) + hq)
+    announce(f"prefill small lens={lens} hq={hq} hkv={hkv}")
+    out = _run(c, gpu, hq, hkv)
+    ref = op.varlen_attention_ref(c.q, c.k, c.v, c.cu_seqlens, c.scale, dtype=torch.float64)
+    assert_close_attn(out, ref, f"lens={lens}")
+    fl = op.flash_varlen_ref(c.q, c.k, c.v, c.cu_seqlens, c.scale)
+    assert_close_attn(out, fl, "vs reference flash restatement")
+
+
+def test_prefill_non_causal(gpu):
+    c = oi.make_prefill_case([40, 90], 16, 8, 128, seed=3)
+    announce("prefill non-causal")
+    out = _run(c, gpu, 16, 8, causal=False)
+    ref = op.varlen_attention_ref(c.q, c.k, c.v, c.cu_seqlens, c.scale, causal=False,
+                                  dtype=torch.float64)
+    assert_close_attn(out, ref, "non-causal")
+
+
+def test_prefill_single_token_sequences_return_v(gpu):
+    c = oi.make_prefill_case([1, 1, 5, 1], 16, 8, 128, seed=4)
+    announce("prefill single-token sequences")
+    out = _run(c, gpu, 16, 8)
+    for s in (0, 1, 3):
+        t = int(c.cu_seqlens[s])
+        for h in range(16):
+            assert torch.equal(out[t, h], c.v[t, h // 2])
+
+
+def test_prefill_config2_vs_fp32(gpu):
+    """Qwen3-0.6B varlen prefill: 8 sequences, lengths uniform in [64, 2048]."""
+    c = oi.config2_prefill()
+    announce(f"prefill config2 lens={c.lens}")
+    out = _run(c, gpu, 16, 8)
+    q, k, v = c.q.to(gpu), c.k.to(gpu), c.v.to(gpu)
+    ref = torch.empty(q.shape, dtype=torch.float32, device=gpu)
+    for s in range(len(c.lens)):
+        s0, s1 = int(c.cu_seqlens[s]), int(c.cu_seqlens[s + 1])
+        L = s1 - s0
+        qs = q[s0:s1].float().transpose(0, 1).contiguous()
+        ks = k[s0:s1].float().transpose(0, 1).repeat_interleave(2, 0)
+        vs = v[s0:s1].float().transpose(0, 1).repeat_interleave(2, 0).contiguous()
+        sc = torch.matmul(qs, ks.transpose(1, 2).contiguous()) * c.scale
+        sc.masked_fill_(~torch.ones(L, L, dtype=torch.bool, device=gpu).tril(), float("-inf"))
+        ref[s0:s1] = torch.matmul(torch.softmax(sc, -1), vs).transpose(0, 1)
+    assert_close_attn(out, ref.cpu(), "config2")
+
+
+def test_prefill_batched_adaptor_pads_zero(gpu):
+    """flash_attention_prefill_batched on a right-padded batch: valid rows
+    match the closed form, pad rows are zero (reference :252-258)."""
+    from qwen3_engine_from_scratch_amd.kernels.flash_attention_varlen import \
+        flash_attention_prefill_batched
+
+    lens, S = [5, 48, 31], 48
+    c = oi.make_prefill_case(lens, 16, 8, 128, seed=5)
+    qp = op.pad_batch(c.q, c.cu_seqlens, S).to(gpu)
+    kp = op.pad_batch(c.k, c.cu_seqlens, S).to(gpu)
+    vp = op.pad_batch(c.v, c.cu_seqlens, S).to(gpu)
+    announce("prefill batched adaptor")
+    out = flash_attention_prefill_batched(qp, kp, vp, lens, c.scale, 16, 8, 128).cpu()
+    out = out.view(3, S, 16, 128)
+    ref = op.varlen_attention_ref(c.q, c.k, c.v, c.cu_seqlens, c.scale, dtype=torch.float64)
+    for b, L in enumerate(lens):
+        s0 = int(c.cu_seqlens[b])
+        assert_close_attn(out[b, :L], ref[s0:s0 + L], f"row {b}")
+        assert not out[b, L:].any()
