@@ -81,11 +81,15 @@ int qwen3_attn_abi_version(void);
  *   seq_lens   int32 (max_rows,)
  *   row_ids    int32 (B,) or NULL (identity)
  *   workspace  device scratch of at least qwen3_paged_decode_workspace_bytes()
- *              bytes (split-KV partials); its size depends only on
- *              (B, num_heads, head_dim, max_pages, block_size), never on the
- *              live lengths, so one launch shape serves a captured graph.
+ *              bytes, 16-byte aligned (split-KV partials); its size depends
+ *              only on (B, num_heads, head_dim, max_pages, block_size), never
+ *              on the live lengths, so one launch shape serves a captured
+ *              graph.  Its contents need no initialisation.
  * Supported: head_dim 128, block_size a multiple of 16,
- *            num_heads / num_kv_heads in [1, 16].
+ *            num_heads / num_kv_heads in [1, 16]; q, K, V and out rows
+ *            16-byte aligned (strides multiples of 8 elements).
+ * Launches two kernels on `stream` (the attention pass and a small merge of
+ * sequences split across waves).
  * ---------------------------------------------------------------------- */
 size_t qwen3_paged_decode_workspace_bytes(int B, int num_heads, int head_dim,
                                           int64_t max_pages, int block_size);

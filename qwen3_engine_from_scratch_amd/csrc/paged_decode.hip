@@ -7,15 +7,18 @@
 // through block_table[row]; softmax in fp32, bf16 output.
 //
 // Design (MI355X-first, not a transcription of the Triton program):
-//  * Work unit = (partition of 16-token tiles, kv head, batch entry): one
-//    256-thread workgroup (4 wave64s).  A partition covers TILES_PER_WAVE
-//    tiles per wave; long contexts therefore split into many workgroups
-//    (split-KV), and a second kernel merges partitions with log-sum-exp
-//    weights.  Single-partition sequences are written directly.
-//  * A 16-token tile of one KV head is 4 KiB of K and 4 KiB of V, contiguous
-//    in the pool; every lane issues 16-byte loads (4 for K, 4 for V), all
-//    loads of a chunk of tiles are issued before any math so a wave keeps
-//    up to 32 KiB in flight.
+//  * The work is the flat list of (sequence, KV head, 16-token tile) triples.
+//    A persistent grid of two 256-thread workgroups per CU splits that list
+//    into equal contiguous ranges, one per wave (stream-KV): every wave
+//    streams the same number of tiles, so there is no tail imbalance and no
+//    per-workgroup start-up cost beyond one prologue.  A sequence-head that
+//    straddles two waves' ranges is finished by a small merge kernel
+//    (log-sum-exp weights); at most two partials exist per wave.
+//  * A tile of one KV head is 4 KiB of K plus 4 KiB of V, contiguous in the
+//    pool.  Each lane issues 16-byte loads (4 for K, 4 for V); a wave keeps
+//    two batches of kChunk tiles in flight while it computes the previous
+//    batch (software pipeline), and prefetches the next 64 block-table
+//    entries before it needs them.
 //  * QK^T on the matrix cores: S^T(16 tok x 16 q) = K(16x128) Q^T(128x16)
 //    as 4 x mfma_f32_16x16x32_bf16.  The G query heads fill G of the 16
 //    columns (zero-padded Q); padding costs idle MFMA slots, not registers.
@@ -25,17 +28,28 @@
 //    8 x mfma_f32_16x16x16_bf16, where the V^T operand is built in-lane
 //    from the row-major 16-byte V loads with byte permutes.
 //  * Online softmax in the exp2 domain, one running max per query column,
-//    updated once per chunk of tiles.
+//    updated once per batch of tiles.
+//  * Batches above kStreamMaxB use a non-persistent grid variant (one
+//    workgroup per partition of tiles) with the same tile math.
 #include "common.hpp"
 
 namespace {
 
-constexpr int kD = 128;      // head_dim
-constexpr int kTile = 16;    // tokens per MFMA tile
-constexpr int kWaves = 4;    // waves per workgroup
-constexpr int kChunk = 4;    // tiles whose loads are in flight together per wave
-constexpr int kMaxG = 16;    // query heads per KV head (MFMA columns)
-constexpr int kOStride = kD + 4;  // padded LDS row of the partition output
+constexpr int kD = 128;        // head_dim
+constexpr int kTile = 16;      // tokens per MFMA tile
+constexpr int kWaves = 4;      // waves per workgroup
+constexpr int kChunk = 2;      // tiles per load batch; two batches in flight per wave
+constexpr int kMaxG = 16;      // query heads per KV head (MFMA columns)
+constexpr int kWin = 64;       // block-table entries held per window (one per lane)
+// Persistent (stream) path.
+constexpr int kStreamMaxB = 2048;       // batch entries tabulated in LDS
+constexpr int kStreamWgPerCu = 2;       // resident workgroups per CU (2 waves/SIMD)
+constexpr int kStreamMaxWgs = 1024;     // workspace sized for up to 512 CUs
+constexpr int kMinTilesPerWave = 16;
+// Grid path (large batches).
+constexpr int kGridTilesPerWave = 32;
+constexpr int kGridTilesPerPart = kGridTilesPerWave * kWaves;
+constexpr int kOStride = kD + 4;  // padded LDS row of a wave's partition output
 
 struct DecodeArgs {
   const uint16_t* q;
@@ -54,41 +68,528 @@ struct DecodeArgs {
   int64_t o_sb, o_sh;
   int B, Hq, Hkv, G, bs;
   float scale_log2;  // softmax scale * log2(e)
+  // stream path workspace
+  float* s_po;       // [W][2][kMaxG][kD] normalised partial outputs
+  float* s_plse;     // [W][2][kMaxG] log2-sum-exp of each partial
+  int32_t* s_pref;   // [B + 1] exclusive prefix of tiles per sequence
+  int32_t* s_meta;   // [0] tiles per wave
+  // grid path workspace
   int max_parts;     // partitions per (b, hkv) the workspace is sized for
   float* ws_o;       // [B][Hq][max_parts][kD] normalised partition outputs
-  float* ws_lse;     // [B][Hq][max_parts] log2-sum-exp of each partition
+  float* ws_lse;     // [B][Hq][max_parts]
 };
 
-// Context length (tokens) of batch entry b, clamped to what the table row can
-// address; 0 for an out-of-range row id.
-__device__ __forceinline__ int64_t context_len(const DecodeArgs& a, int b, int64_t* row_out) {
+// Row of batch entry b in the resident tables, or -1 if out of range.
+__device__ __forceinline__ int64_t row_of(const DecodeArgs& a, int b) {
   const int64_t row = a.row_ids ? a.row_ids[b] : b;
-  *row_out = row;
-  if (row < 0 || row >= a.max_rows) return 0;
-  int64_t L = static_cast<int64_t>(a.seq_lens[row]) + a.bias;
+  return (row >= 0 && row < a.max_rows) ? row : -1;
+}
+
+// Context length of a valid row, clamped to what one table row addresses.
+__device__ __forceinline__ int64_t clamp_len(const DecodeArgs& a, int32_t seq_len) {
+  int64_t L = static_cast<int64_t>(seq_len) + a.bias;
   const int64_t cap = a.max_pages * a.bs;
   L = L < cap ? L : cap;
   return L > 0 ? L : 0;
 }
 
-template <int TILES_PER_WAVE>
-__global__ __launch_bounds__(kWaves * 64) void paged_decode_part_kernel(DecodeArgs a) {
-  constexpr int kTilesPerPart = TILES_PER_WAVE * kWaves;
+// ---------------------------------------------------------------------------
+// Tile math shared by both paths.
+
+// K/V registers of up to kChunk 16-token tiles of one KV head of one sequence.
+//   k[i][c]: token lo of tile i, dims c*32 + 8*hi .. +7   (A operand of QK^T)
+//   v[i][e]: token 4*hi + e of tile i, dims 8*lo .. +7    (row-major V rows)
+struct Chunk {
+  q3::u32x4 k[kChunk][4];
+  q3::u32x4 v[kChunk][4];
+  bool valid[kChunk];
+  int n;       // tiles in this batch (0 = none)
+  int t0;      // first tile (index within the sequence)
+  int seg;     // b * Hkv + hkv
+  int ntiles;  // tiles of the whole sequence
+  int L;       // context length of the sequence
+};
+
+__device__ __forceinline__ void load_tile(Chunk& c, int i, const DecodeArgs& a,
+                                          const uint16_t* kbase, const uint16_t* vbase,
+                                          int64_t phys, int sub, int lo, int hi) {
+  c.valid[i] = phys >= 0 && phys < a.num_blocks;
+  if (c.valid[i]) {
+    const uint16_t* kp = kbase + phys * a.k_sblk + (sub + lo) * a.k_sslot + hi * 8;
+#pragma unroll
+    for (int cc = 0; cc < 4; ++cc) c.k[i][cc] = q3::ld16(kp + cc * 32);
+    const uint16_t* vp = vbase + phys * a.v_sblk + (sub + 4 * hi) * a.v_sslot + lo * 8;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) c.v[i][e] = q3::ld16(vp + e * a.v_sslot);
+  } else {
+#pragma unroll
+    for (int cc = 0; cc < 4; ++cc) {
+      c.k[i][cc] = q3::u32x4{0u, 0u, 0u, 0u};
+      c.v[i][cc] = q3::u32x4{0u, 0u, 0u, 0u};
+    }
+  }
+}
+
+struct SoftmaxState {
+  float m;           // running max (log2 domain) of column lo
+  float l;           // this lane's share of the running denominator
+  q3::f32x4 acc[8];  // acc[j][r] = O[lo][32*hi + 8*r + j] (unnormalised)
+};
+
+__device__ __forceinline__ void reset(SoftmaxState& st) {
+  st.m = q3::kNegInf;
+  st.l = 0.f;
+#pragma unroll
+  for (int j = 0; j < 8; ++j) st.acc[j] = q3::f32x4{0.f, 0.f, 0.f, 0.f};
+}
+
+// Q^T as the B operand: lane (column lo, k-group hi) holds, for chunk c of 32
+// dims, the 8 dims c*32 + hi*8 .. +7 of query head hkv*G + lo (zero if lo >= G).
+__device__ __forceinline__ void load_q(q3::bf16x8 (&qv)[4], const DecodeArgs& a, int b, int hkv,
+                                       int lo, int hi) {
+  q3::u32x4 z = {0u, 0u, 0u, 0u};
+  if (lo < a.G) {
+    const uint16_t* qp =
+        a.q + b * a.q_sb + (static_cast<int64_t>(hkv) * a.G + lo) * a.q_sh + hi * 8;
+#pragma unroll
+    for (int c = 0; c < 4; ++c) qv[c] = q3::as_bf16x8(q3::ld16(qp + c * 32));
+  } else {
+#pragma unroll
+    for (int c = 0; c < 4; ++c) qv[c] = q3::as_bf16x8(z);
+  }
+}
+
+// Folds c.n tiles (first tile c.t0) into the online softmax state.
+__device__ __forceinline__ void compute_chunk(Chunk& c, float scale_log2, int hi,
+                                              const q3::bf16x8 (&qv)[4], SoftmaxState& st) {
+  // S^T = K Q^T: lane (column lo, k-group hi) receives tokens 4*hi + r.
+  q3::f32x4 s[kChunk];
+#pragma unroll
+  for (int i = 0; i < kChunk; ++i) {
+    s[i] = q3::f32x4{0.f, 0.f, 0.f, 0.f};
+    if (i < c.n) {
+#pragma unroll
+      for (int cc = 0; cc < 4; ++cc)
+        s[i] = q3::mfma16x16x32(q3::as_bf16x8(c.k[i][cc]), qv[cc], s[i]);
+    }
+  }
+  float mx = q3::kNegInf;
+#pragma unroll
+  for (int i = 0; i < kChunk; ++i) {
+    const int tokb = (c.t0 + i) * kTile + 4 * hi;
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const bool ok = i < c.n && c.valid[i] && tokb + r < c.L;
+      const float v = ok ? s[i][r] * scale_log2 : q3::kNegInf;
+      s[i][r] = v;
+      mx = fmaxf(mx, v);
+      // A slot at or past L may hold anything (even NaN): its P is 0, but
+      // 0 * NaN is not, so the V row of such a slot is zeroed.
+      if (!ok) c.v[i][r] = q3::u32x4{0u, 0u, 0u, 0u};
+    }
+  }
+  mx = fmaxf(mx, q3::shfl_xor(mx, 16));
+  mx = fmaxf(mx, q3::shfl_xor(mx, 32));
+  const float m_new = fmaxf(st.m, mx);
+  const float m_use = m_new == q3::kNegInf ? 0.f : m_new;
+  const float alpha = q3::fast_exp2(st.m - m_use);
+  st.m = m_new;
+
+  q3::bf16x4 p[kChunk];
+  float psum = 0.f;
+#pragma unroll
+  for (int i = 0; i < kChunk; ++i) {
+    float e[4];
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      e[r] = q3::fast_exp2(s[i][r] - m_use);
+      psum += e[r];
+    }
+    q3::u32x2 pk = {q3::pack_bf16x2(e[0], e[1]), q3::pack_bf16x2(e[2], e[3])};
+    p[i] = q3::as_bf16x4(pk);
+  }
+  st.l = st.l * alpha + psum;
+#pragma unroll
+  for (int j = 0; j < 8; ++j) st.acc[j] *= alpha;
+
+  // O^T += V^T P^T.  For output slice j the A operand of lane (dim group lo,
+  // k-group hi) is V[4*hi + e][8*lo + j], e = 0..3, gathered from the four
+  // row-major 16-byte V loads of the lane.
+#pragma unroll
+  for (int i = 0; i < kChunk; ++i) {
+    if (i < c.n) {
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        const int w = j >> 1, h = j & 1;
+        q3::u32x2 av = {q3::pick_halves(c.v[i][0][w], c.v[i][1][w], h),
+                        q3::pick_halves(c.v[i][2][w], c.v[i][3][w], h)};
+        st.acc[j] = q3::mfma16x16x16(q3::as_bf16x4(av), p[i], st.acc[j]);
+      }
+    }
+  }
+}
+
+// Completes the per-column denominator (lanes of one column hold disjoint
+// token subsets) and returns 1/l (0 for an empty column).
+__device__ __forceinline__ float finish_l(SoftmaxState& st) {
+  st.l += q3::shfl_xor(st.l, 16);
+  st.l += q3::shfl_xor(st.l, 32);
+  return st.l > 0.f ? 1.f / st.l : 0.f;
+}
+
+// Writes the normalised output of column lo (a query head) as bf16: lane
+// (lo, hi) owns dims 32*hi .. 32*hi + 31.
+__device__ __forceinline__ void store_out_bf16(const DecodeArgs& a, int b, int hq,
+                                               const SoftmaxState& st, float inv, int hi) {
+  uint16_t* op = a.out + b * a.o_sb + static_cast<int64_t>(hq) * a.o_sh + 32 * hi;
+#pragma unroll
+  for (int r = 0; r < 4; ++r) {
+    q3::u32x4 w = {q3::pack_bf16x2(st.acc[0][r] * inv, st.acc[1][r] * inv),
+                   q3::pack_bf16x2(st.acc[2][r] * inv, st.acc[3][r] * inv),
+                   q3::pack_bf16x2(st.acc[4][r] * inv, st.acc[5][r] * inv),
+                   q3::pack_bf16x2(st.acc[6][r] * inv, st.acc[7][r] * inv)};
+    q3::st16(op + 8 * r, w);
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Stream path: persistent waves over the flat tile list.
+
+// Wave-uniform window of kWin block-table entries of one row (lane i holds
+// entry base + i) plus the prefetched next window.
+struct TableWindow {
+  int64_t row;
+  int base;
+  int32_t cur, next;
+};
+
+__device__ __forceinline__ int32_t table_entry(const DecodeArgs& a, int64_t row, int page) {
+  return (row >= 0 && page < a.max_pages) ? a.bt[row * a.bt_stride + page] : -1;
+}
+
+__device__ __forceinline__ void window_load(TableWindow& tw, const DecodeArgs& a, int64_t row,
+                                            int base, int lane) {
+  tw.row = row;
+  tw.base = base;
+  tw.cur = table_entry(a, row, base + lane);
+  tw.next = table_entry(a, row, base + kWin + lane);
+}
+
+// Physical block of `page` of row tw.row (wave-uniform).
+__device__ __forceinline__ int64_t window_phys(TableWindow& tw, const DecodeArgs& a, int page,
+                                               int lane) {
+  if (page >= tw.base + kWin && page < tw.base + 2 * kWin) {
+    tw.cur = tw.next;
+    tw.base += kWin;
+    tw.next = table_entry(a, tw.row, tw.base + kWin + lane);
+  } else if (page < tw.base || page >= tw.base + kWin) {
+    window_load(tw, a, tw.row, page, lane);
+  }
+  return __builtin_amdgcn_readlane(tw.cur, page - tw.base);
+}
+
+// Load-side cursor of a wave: the next tile to fetch in the flat list.
+struct Cursor {
+  int64_t g, g1;   // global tile index of the next tile, end of the wave's range
+  int b, hkv, t;   // its (sequence, KV head, tile)
+  int n;           // tiles of sequence b
+  int L;           // context length of sequence b
+};
+
+__global__ __launch_bounds__(kWaves * 64) __attribute__((amdgpu_waves_per_eu(2, 2)))
+void paged_decode_stream_kernel(DecodeArgs a) {
+  __shared__ int32_t s_pref[kStreamMaxB + 1];
+  __shared__ int32_t s_row[kStreamMaxB];
+  __shared__ int32_t s_len[kStreamMaxB];
+  __shared__ int32_t s_wsum[kWaves];
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = tid >> 6;
+  const int lo = lane & 15;
+  const int hi = lane >> 4;
+  const int B = a.B;
+
+  // ---- prologue: rows, lengths and the exclusive tile prefix of every sequence ----
+  constexpr int kPer = kStreamMaxB / (kWaves * 64);
+  int cnt[kPer];
+  int local = 0;
+#pragma unroll
+  for (int i = 0; i < kPer; ++i) {
+    const int b = tid * kPer + i;
+    int n = 0;
+    if (b < B) {
+      const int64_t row = row_of(a, b);
+      const int64_t L = row >= 0 ? clamp_len(a, a.seq_lens[row]) : 0;
+      s_row[b] = static_cast<int32_t>(row);
+      s_len[b] = static_cast<int32_t>(L);
+      n = static_cast<int>(q3::cdiv(L, kTile));
+    }
+    cnt[i] = n;
+    local += n;
+  }
+  int incl = local;
+#pragma unroll
+  for (int o = 1; o < 64; o <<= 1) {
+    const int y = __shfl_up(incl, o, 64);
+    if (lane >= o) incl += y;
+  }
+  if (lane == 63) s_wsum[wave] = incl;
+  __syncthreads();
+  int run = incl - local;
+  int total = 0;
+#pragma unroll
+  for (int w = 0; w < kWaves; ++w) {
+    if (w < wave) run += s_wsum[w];
+    total += s_wsum[w];
+  }
+#pragma unroll
+  for (int i = 0; i < kPer; ++i) {
+    const int b = tid * kPer + i;
+    if (b < B) s_pref[b] = run;
+    run += cnt[i];
+  }
+  if (tid == 0) s_pref[B] = total;
+  __syncthreads();
+
+  const int64_t T = static_cast<int64_t>(a.Hkv) * total;
+  const int64_t W = static_cast<int64_t>(gridDim.x) * kWaves;
+  int64_t pw = q3::cdiv(T, W);
+  pw = pw < kMinTilesPerWave ? kMinTilesPerWave : pw;
+  if (blockIdx.x == 0) {
+    for (int b = tid; b <= B; b += kWaves * 64) a.s_pref[b] = s_pref[b];
+    if (tid == 0) a.s_meta[0] = static_cast<int32_t>(pw);
+  }
+  const int64_t w = static_cast<int64_t>(blockIdx.x) * kWaves + wave;
+  const int64_t g0 = w * pw;
+  if (g0 >= T) return;
+
+  // ---- locate the wave's first tile: largest b with Hkv * pref[b] <= g0 ----
+  Cursor cur;
+  {
+    int lo_b = 0, hi_b = B - 1;
+    while (lo_b < hi_b) {
+      const int mid = (lo_b + hi_b + 1) >> 1;
+      if (static_cast<int64_t>(a.Hkv) * s_pref[mid] <= g0) lo_b = mid; else hi_b = mid - 1;
+    }
+    cur.b = lo_b;
+    cur.n = s_pref[lo_b + 1] - s_pref[lo_b];
+    cur.L = s_len[lo_b];
+    const int64_t off = g0 - static_cast<int64_t>(a.Hkv) * s_pref[lo_b];
+    cur.hkv = static_cast<int>(off / cur.n);
+    cur.t = static_cast<int>(off % cur.n);
+    cur.g = g0;
+    cur.g1 = g0 + pw < T ? g0 + pw : T;
+  }
+  TableWindow tw;
+  window_load(tw, a, s_row[cur.b], (cur.t * kTile) / a.bs, lane);
+
+  // Issues the next batch of at most kChunk tiles of the current sequence-head.
+  auto issue = [&](Chunk& c) {
+    c.n = 0;
+    if (cur.g >= cur.g1) return;
+    if (cur.t >= cur.n) {  // next sequence-head
+      if (++cur.hkv == a.Hkv) {
+        cur.hkv = 0;
+        do {
+          ++cur.b;
+        } while (s_pref[cur.b + 1] == s_pref[cur.b]);
+        cur.n = s_pref[cur.b + 1] - s_pref[cur.b];
+        cur.L = s_len[cur.b];
+      }
+      cur.t = 0;
+      tw.row = s_row[cur.b];
+      window_load(tw, a, tw.row, 0, lane);
+    }
+    int64_t left = cur.g1 - cur.g;
+    int n = cur.n - cur.t;
+    n = n < kChunk ? n : kChunk;
+    n = left < n ? static_cast<int>(left) : n;
+    c.n = n;
+    c.t0 = cur.t;
+    c.seg = cur.b * a.Hkv + cur.hkv;
+    c.ntiles = cur.n;
+    c.L = cur.L;
+    const uint16_t* kbase = a.k + static_cast<int64_t>(cur.hkv) * a.k_sh;
+    const uint16_t* vbase = a.v + static_cast<int64_t>(cur.hkv) * a.v_sh;
+#pragma unroll
+    for (int i = 0; i < kChunk; ++i) {
+      int64_t phys = -1;
+      int sub = 0;
+      if (i < n) {
+        const int tok0 = (cur.t + i) * kTile;
+        phys = window_phys(tw, a, tok0 / a.bs, lane);
+        sub = tok0 % a.bs;
+      }
+      load_tile(c, i, a, kbase, vbase, phys, sub, lo, hi);
+    }
+    cur.t += n;
+    cur.g += n;
+  };
+
+  // Compute-side state: the sequence-head being accumulated.
+  int cseg = -1, cb = 0, chkv = 0, ct_lo = 0, ct_hi = 0, cn = 0;
+  bool cfirst = true;
+  q3::bf16x8 qv[4];
+  SoftmaxState st;
+  reset(st);
+
+  auto finalize = [&]() {
+    const float inv = finish_l(st);
+    const bool complete = ct_lo == 0 && ct_hi == cn;
+    if (lo < a.G) {
+      const int hq = chkv * a.G + lo;
+      if (complete) {
+        store_out_bf16(a, cb, hq, st, inv, hi);
+      } else {
+        const int64_t slot = (w * 2 + (cfirst ? 0 : 1)) * kMaxG + lo;
+        float* po = a.s_po + slot * kD + 32 * hi;
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          q3::f32x4 v0 = {st.acc[0][r] * inv, st.acc[1][r] * inv, st.acc[2][r] * inv,
+                          st.acc[3][r] * inv};
+          q3::f32x4 v1 = {st.acc[4][r] * inv, st.acc[5][r] * inv, st.acc[6][r] * inv,
+                          st.acc[7][r] * inv};
+          *reinterpret_cast<q3::f32x4*>(po + 8 * r) = v0;
+          *reinterpret_cast<q3::f32x4*>(po + 8 * r + 4) = v1;
+        }
+        if (hi == 0) a.s_plse[slot] = st.l > 0.f ? st.m + __builtin_log2f(st.l) : q3::kNegInf;
+      }
+    }
+  };
+
+  auto process = [&](Chunk& c) {
+    if (c.seg != cseg) {
+      if (cseg >= 0) {
+        finalize();
+        cfirst = false;
+      }
+      cseg = c.seg;
+      cb = c.seg / a.Hkv;
+      chkv = c.seg % a.Hkv;
+      ct_lo = c.t0;
+      cn = c.ntiles;
+      load_q(qv, a, cb, chkv, lo, hi);
+      reset(st);
+    }
+    compute_chunk(c, a.scale_log2, hi, qv, st);
+    ct_hi = c.t0 + c.n;
+  };
+
+  Chunk ca, cbuf;
+  issue(ca);
+  issue(cbuf);
+  while (true) {
+    if (ca.n == 0) break;
+    process(ca);
+    issue(ca);
+    if (cbuf.n == 0) break;
+    process(cbuf);
+    issue(cbuf);
+  }
+  if (cseg >= 0) finalize();
+}
+
+// Combines the partials of every sequence-head split across waves and
+// writes zeros for empty contexts.  One workgroup per (kv head, batch entry)
+// with one wave per query head of the group: lanes first fetch the LSEs of up
+// to 64 covering waves at once, then every lane owns two output dims and sums
+// the weighted partials kBatch waves at a time.
+__global__ __launch_bounds__(kMaxG * 64) void paged_decode_stream_merge_kernel(DecodeArgs a) {
+  constexpr int kBatch = 8;
+  const int hkv = blockIdx.x;
+  const int b = blockIdx.y;
+  const int lane = threadIdx.x & 63;
+  const int g = threadIdx.x >> 6;  // query head within the group
+  const int G = a.G;
+  if (g >= G) return;
+  const int64_t pref_b = a.s_pref[b];
+  const int n = a.s_pref[b + 1] - static_cast<int32_t>(pref_b);
+  const int64_t hq = static_cast<int64_t>(hkv) * G + g;
+  uint32_t* op = reinterpret_cast<uint32_t*>(a.out + b * a.o_sb + hq * a.o_sh + 2 * lane);
+  if (n == 0) {
+    *op = 0u;
+    return;
+  }
+  const int64_t pw = a.s_meta[0];
+  const int64_t S = static_cast<int64_t>(a.Hkv) * pref_b + static_cast<int64_t>(hkv) * n;
+  const int64_t E = S + n;
+  const int64_t wf = S / pw, wl = (E - 1) / pw;
+  if (wf == wl) return;  // written whole by its wave
+  const int nw = static_cast<int>(wl - wf + 1);
+  auto slot_of = [&](int i) -> int64_t {
+    const int64_t wv = wf + i;
+    const int half = (i == 0 && wv * pw != S) ? 1 : 0;
+    return (wv * 2 + half) * kMaxG + g;
+  };
+  // Pass 1: global max of the partial LSEs.
+  float M = q3::kNegInf;
+  for (int i0 = 0; i0 < nw; i0 += 64)
+    if (i0 + lane < nw) M = fmaxf(M, a.s_plse[slot_of(i0 + lane)]);
+#pragma unroll
+  for (int o = 32; o >= 1; o >>= 1) M = fmaxf(M, q3::shfl_xor(M, o));
+  const float M_use = M == q3::kNegInf ? 0.f : M;
+  // Pass 2: weighted sum of the partial outputs (lane owns dims 2*lane, 2*lane+1).
+  float sw = 0.f, o0 = 0.f, o1 = 0.f;
+  for (int i0 = 0; i0 < nw; i0 += 64) {
+    const float wl_lane = (i0 + lane < nw) ? q3::fast_exp2(a.s_plse[slot_of(i0 + lane)] - M_use) : 0.f;
+    float wsum = wl_lane;
+#pragma unroll
+    for (int o = 32; o >= 1; o >>= 1) wsum += q3::shfl_xor(wsum, o);
+    sw += wsum;
+    const int cnt = nw - i0 < 64 ? nw - i0 : 64;
+    for (int j0 = 0; j0 < cnt; j0 += kBatch) {
+      float2 ov[kBatch];
+      float wt[kBatch];
+#pragma unroll
+      for (int j = 0; j < kBatch; ++j) {
+        const bool ok = j0 + j < cnt;
+        wt[j] = __shfl(wl_lane, ok ? j0 + j : 0, 64);
+        ov[j] = ok ? *reinterpret_cast<const float2*>(a.s_po + slot_of(i0 + j0 + j) * kD + 2 * lane)
+                   : float2{0.f, 0.f};
+        wt[j] = ok ? wt[j] : 0.f;
+      }
+#pragma unroll
+      for (int j = 0; j < kBatch; ++j) {
+        o0 += wt[j] * ov[j].x;
+        o1 += wt[j] * ov[j].y;
+      }
+    }
+  }
+  const float inv = sw > 0.f ? 1.f / sw : 0.f;
+  *op = q3::pack_bf16x2(o0 * inv, o1 * inv);
+}
+
+// ---------------------------------------------------------------------------
+// Grid path (batches above kStreamMaxB): one workgroup per partition of
+// kGridTilesPerPart tiles of one sequence-head; waves combine through LDS.
+
+__global__ __launch_bounds__(kWaves * 64) __attribute__((amdgpu_waves_per_eu(2, 2)))
+void paged_decode_grid_kernel(DecodeArgs a) {
   const int part = blockIdx.x;
   const int hkv = blockIdx.y;
   const int b = blockIdx.z;
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = tid >> 6;
-  const int lo = lane & 15;  // q column (QK/PV) or token row (K operand) or dim group (V)
-  const int hi = lane >> 4;  // k-group
-
-  int64_t row;
-  const int64_t L = context_len(a, b, &row);
-  const int n_tiles = static_cast<int>(q3::cdiv(L, kTile));
-  const int tile0 = part * kTilesPerPart;
+  const int lo = lane & 15;
+  const int hi = lane >> 4;
   const int G = a.G;
 
+  const int64_t row = row_of(a, b);
+  const int tile0 = part * kGridTilesPerPart;
+  const int w0 = tile0 + wave * kGridTilesPerWave;
+  int32_t seq_len = 0;
+  TableWindow tw;
+  tw.row = row;
+  tw.base = (w0 * kTile) / a.bs;
+  tw.cur = -1;
+  tw.next = -1;
+  if (row >= 0) {
+    seq_len = a.seq_lens[row];
+    tw.cur = table_entry(a, row, tw.base + lane);
+  }
+  const int L = static_cast<int>(row >= 0 ? clamp_len(a, seq_len) : 0);
+  const int n_tiles = static_cast<int>(q3::cdiv(L, kTile));
   if (tile0 >= n_tiles) {
     if (part == 0) {  // empty context: defined zero output
       for (int e = tid; e < G * kD; e += kWaves * 64) {
@@ -98,177 +599,91 @@ __global__ __launch_bounds__(kWaves * 64) void paged_decode_part_kernel(DecodeAr
     }
     return;
   }
-  const int n_parts = static_cast<int>(q3::cdiv(n_tiles, kTilesPerPart));
-  const int tile_end = min(n_tiles, tile0 + kTilesPerPart);
+  const int n_parts = static_cast<int>(q3::cdiv(n_tiles, kGridTilesPerPart));
+  const int w1 = min(min(n_tiles, tile0 + kGridTilesPerPart), w0 + kGridTilesPerWave);
+  const uint16_t* kbase = a.k + static_cast<int64_t>(hkv) * a.k_sh;
+  const uint16_t* vbase = a.v + static_cast<int64_t>(hkv) * a.v_sh;
+
+  int t_next = w0;
+  auto issue = [&](Chunk& c) {
+    c.n = 0;
+    if (t_next >= w1) return;
+    const int n = min(kChunk, w1 - t_next);
+    c.n = n;
+    c.t0 = t_next;
+    c.L = L;
+#pragma unroll
+    for (int i = 0; i < kChunk; ++i) {
+      int64_t phys = -1;
+      int sub = 0;
+      if (i < n) {
+        const int tok0 = (t_next + i) * kTile;
+        // kGridTilesPerWave tiles span at most kWin pages (block_size >= 16).
+        phys = __builtin_amdgcn_readlane(tw.cur, tok0 / a.bs - tw.base);
+        sub = tok0 % a.bs;
+      }
+      load_tile(c, i, a, kbase, vbase, phys, sub, lo, hi);
+    }
+    t_next += n;
+  };
+
+  Chunk ca, cbuf;
+  issue(ca);
+  issue(cbuf);
+  q3::bf16x8 qv[4];
+  load_q(qv, a, b, hkv, lo, hi);
+  SoftmaxState st;
+  reset(st);
+  while (true) {
+    if (ca.n == 0) break;
+    compute_chunk(ca, a.scale_log2, hi, qv, st);
+    issue(ca);
+    if (cbuf.n == 0) break;
+    compute_chunk(cbuf, a.scale_log2, hi, qv, st);
+    issue(cbuf);
+  }
+  st.l += q3::shfl_xor(st.l, 16);
+  st.l += q3::shfl_xor(st.l, 32);
 
   __shared__ float s_m[kWaves][kMaxG];
   __shared__ float s_l[kWaves][kMaxG];
-  __shared__ float s_o[kMaxG * kOStride];
-  for (int e = tid; e < G * kOStride; e += kWaves * 64) s_o[e] = 0.f;
-
-  // Q^T as the B operand: lane (column lo, k-group hi) holds, for chunk c of
-  // 32 dims, the 8 dims c*32 + hi*8 .. +7 of query head hkv*G + lo.
-  q3::bf16x8 qv[4];
-  {
-    q3::u32x4 z = {0u, 0u, 0u, 0u};
-    if (lo < G) {
-      const uint16_t* qp = a.q + b * a.q_sb + (static_cast<int64_t>(hkv) * G + lo) * a.q_sh + hi * 8;
-#pragma unroll
-      for (int c = 0; c < 4; ++c) qv[c] = q3::as_bf16x8(q3::ld16(qp + c * 32));
-    } else {
-#pragma unroll
-      for (int c = 0; c < 4; ++c) qv[c] = q3::as_bf16x8(z);
-    }
-  }
-
-  float m_run = q3::kNegInf;  // running max (log2 domain) of column lo
-  float l_run = 0.f;          // this lane's share of the running denominator
-  q3::f32x4 acc[8];           // acc[j][r] = O[lo][32*hi + 8*r + j] (unnormalised)
-#pragma unroll
-  for (int j = 0; j < 8; ++j) acc[j] = q3::f32x4{0.f, 0.f, 0.f, 0.f};
-
-  const int w0 = tile0 + wave * TILES_PER_WAVE;
-  const int w1 = min(tile_end, w0 + TILES_PER_WAVE);
-  const uint16_t* kbase = a.k + static_cast<int64_t>(hkv) * a.k_sh;
-  const uint16_t* vbase = a.v + static_cast<int64_t>(hkv) * a.v_sh;
-  const int32_t* bt_row = a.bt + row * a.bt_stride;
-
-  for (int t0 = w0; t0 < w1; t0 += kChunk) {
-    q3::u32x4 kr[kChunk][4];
-    q3::u32x4 vr[kChunk][4];
-    bool tv[kChunk];
-#pragma unroll
-    for (int i = 0; i < kChunk; ++i) {
-      const int t = t0 + i;
-      int64_t phys = -1;
-      int sub = 0;
-      if (t < w1) {
-        const int64_t tok0 = static_cast<int64_t>(t) * kTile;
-        phys = bt_row[tok0 / a.bs];
-        sub = static_cast<int>(tok0 % a.bs);
-      }
-      tv[i] = phys >= 0 && phys < a.num_blocks;
-      if (tv[i]) {
-        const uint16_t* kp = kbase + phys * a.k_sblk + (sub + lo) * a.k_sslot + hi * 8;
-#pragma unroll
-        for (int c = 0; c < 4; ++c) kr[i][c] = q3::ld16(kp + c * 32);
-        const uint16_t* vp = vbase + phys * a.v_sblk + (sub + 4 * hi) * a.v_sslot + lo * 8;
-#pragma unroll
-        for (int e = 0; e < 4; ++e) vr[i][e] = q3::ld16(vp + e * a.v_sslot);
-        // Slots at or past L in the last tile may hold anything (even NaN);
-        // their P is 0 but 0 * NaN is not, so zero those V rows.
-        const int64_t tok_e0 = static_cast<int64_t>(t) * kTile + 4 * hi;
-        if (static_cast<int64_t>(t + 1) * kTile > L) {
-#pragma unroll
-          for (int e = 0; e < 4; ++e)
-            if (tok_e0 + e >= L) vr[i][e] = q3::u32x4{0u, 0u, 0u, 0u};
-        }
-      } else {
-#pragma unroll
-        for (int c = 0; c < 4; ++c) {
-          kr[i][c] = q3::u32x4{0u, 0u, 0u, 0u};
-          vr[i][c] = q3::u32x4{0u, 0u, 0u, 0u};
-        }
-      }
-    }
-
-    // S^T = K Q^T: lane (column lo, k-group hi) receives tokens 4*hi + r.
-    q3::f32x4 s[kChunk];
-#pragma unroll
-    for (int i = 0; i < kChunk; ++i) {
-      s[i] = q3::f32x4{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-      for (int c = 0; c < 4; ++c) s[i] = q3::mfma16x16x32(q3::as_bf16x8(kr[i][c]), qv[c], s[i]);
-    }
-
-    float mx = q3::kNegInf;
-#pragma unroll
-    for (int i = 0; i < kChunk; ++i) {
-      const int64_t tokb = static_cast<int64_t>(t0 + i) * kTile + 4 * hi;
-#pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const float x = (tv[i] && tokb + r < L) ? s[i][r] * a.scale_log2 : q3::kNegInf;
-        s[i][r] = x;
-        mx = fmaxf(mx, x);
-      }
-    }
-    mx = fmaxf(mx, q3::shfl_xor(mx, 16));
-    mx = fmaxf(mx, q3::shfl_xor(mx, 32));
-    const float m_new = fmaxf(m_run, mx);
-    const float m_use = m_new == q3::kNegInf ? 0.f : m_new;
-    const float alpha = q3::fast_exp2(m_run - m_use);
-
-    q3::bf16x4 p[kChunk];
-    float psum = 0.f;
-#pragma unroll
-    for (int i = 0; i < kChunk; ++i) {
-      float e[4];
-#pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        e[r] = q3::fast_exp2(s[i][r] - m_use);
-        psum += e[r];
-      }
-      q3::u32x2 pk = {q3::pack_bf16x2(e[0], e[1]), q3::pack_bf16x2(e[2], e[3])};
-      p[i] = q3::as_bf16x4(pk);
-    }
-    l_run = l_run * alpha + psum;
-    m_run = m_new;
-#pragma unroll
-    for (int j = 0; j < 8; ++j) acc[j] *= alpha;
-
-    // O^T += V^T P^T.  For output slice j the A operand of lane (dim group lo,
-    // k-group hi) is V[4*hi + e][8*lo + j], e = 0..3, gathered from the four
-    // row-major 16-byte V loads of the lane.
-#pragma unroll
-    for (int i = 0; i < kChunk; ++i) {
-#pragma unroll
-      for (int j = 0; j < 8; ++j) {
-        const int w = j >> 1, h = j & 1;
-        q3::u32x2 av = {q3::pick_halves(vr[i][0][w], vr[i][1][w], h),
-                        q3::pick_halves(vr[i][2][w], vr[i][3][w], h)};
-        acc[j] = q3::mfma16x16x16(q3::as_bf16x4(av), p[i], acc[j]);
-      }
-    }
-  }
-
-  // Lanes of one column hold disjoint token subsets of the denominator.
-  l_run += q3::shfl_xor(l_run, 16);
-  l_run += q3::shfl_xor(l_run, 32);
-
-  // ---- combine the waves of the workgroup through LDS ----
+  extern __shared__ float s_acc[];  // [kWaves][G][kOStride] per-wave partition outputs
+  // Each wave stores its unnormalised output in its own slice; the writer
+  // threads merge the slices in fixed wave order (bit-reproducible).
   if (hi == 0) {
-    s_m[wave][lo] = m_run;
-    s_l[wave][lo] = l_run;
+    s_m[wave][lo] = st.m;
+    s_l[wave][lo] = st.l;
   }
-  __syncthreads();
-  float M = q3::kNegInf;
-#pragma unroll
-  for (int w = 0; w < kWaves; ++w) M = fmaxf(M, s_m[w][lo]);
-  const float M_use = M == q3::kNegInf ? 0.f : M;
-  const float wgt = q3::fast_exp2(m_run - M_use);
   if (lo < G) {
+    float* dst = s_acc + (wave * G + lo) * kOStride + 32 * hi;
 #pragma unroll
-    for (int j = 0; j < 8; ++j)
-#pragma unroll
-      for (int r = 0; r < 4; ++r)
-        atomicAdd(&s_o[lo * kOStride + 32 * hi + 8 * r + j], acc[j][r] * wgt);
+    for (int r = 0; r < 4; ++r) {
+      q3::f32x4 v0 = {st.acc[0][r], st.acc[1][r], st.acc[2][r], st.acc[3][r]};
+      q3::f32x4 v1 = {st.acc[4][r], st.acc[5][r], st.acc[6][r], st.acc[7][r]};
+      *reinterpret_cast<q3::f32x4*>(dst + 8 * r) = v0;
+      *reinterpret_cast<q3::f32x4*>(dst + 8 * r + 4) = v1;
+    }
   }
   __syncthreads();
-
-  // ---- write: final bf16 output, or a normalised partial + its LSE ----
   for (int e = tid; e < G * (kD / 2); e += kWaves * 64) {
     const int g = e / (kD / 2);
     const int d = 2 * (e % (kD / 2));
     float Mg = q3::kNegInf;
 #pragma unroll
-    for (int w = 0; w < kWaves; ++w) Mg = fmaxf(Mg, s_m[w][g]);
+    for (int wv = 0; wv < kWaves; ++wv) Mg = fmaxf(Mg, s_m[wv][g]);
     const float Mg_use = Mg == q3::kNegInf ? 0.f : Mg;
-    float Lg = 0.f;
+    float Lg = 0.f, o0 = 0.f, o1 = 0.f;
 #pragma unroll
-    for (int w = 0; w < kWaves; ++w) Lg += s_l[w][g] * q3::fast_exp2(s_m[w][g] - Mg_use);
+    for (int wv = 0; wv < kWaves; ++wv) {
+      const float wg = q3::fast_exp2(s_m[wv][g] - Mg_use);
+      const float* src = s_acc + (wv * G + g) * kOStride + d;
+      Lg += s_l[wv][g] * wg;
+      o0 += src[0] * wg;
+      o1 += src[1] * wg;
+    }
     const float inv = Lg > 0.f ? 1.f / Lg : 0.f;
-    const float o0 = s_o[g * kOStride + d] * inv;
-    const float o1 = s_o[g * kOStride + d + 1] * inv;
+    o0 *= inv;
+    o1 *= inv;
     const int64_t hq = static_cast<int64_t>(hkv) * G + g;
     if (n_parts == 1) {
       *reinterpret_cast<uint32_t*>(a.out + b * a.o_sb + hq * a.o_sh + d) = q3::pack_bf16x2(o0, o1);
@@ -281,39 +696,89 @@ __global__ __launch_bounds__(kWaves * 64) void paged_decode_part_kernel(DecodeAr
   }
 }
 
-// Merges the partitions of every (b, query head) whose context needed more
-// than one: o = sum_p 2^(lse_p - lse_max) o_p / sum_p 2^(lse_p - lse_max).
-template <int TILES_PER_WAVE>
-__global__ __launch_bounds__(kD) void paged_decode_reduce_kernel(DecodeArgs a) {
-  constexpr int kTilesPerPart = TILES_PER_WAVE * kWaves;
+// Merges the partitions of every (b, query head) of the grid path whose
+// context needed more than one.  Loads are batched kBatch partitions at a time.
+__global__ __launch_bounds__(kD) void paged_decode_grid_merge_kernel(DecodeArgs a) {
+  constexpr int kBatch = 8;
   const int hq = blockIdx.x;
   const int b = blockIdx.y;
   const int d = threadIdx.x;
-  int64_t row;
-  const int64_t L = context_len(a, b, &row);
+  const int64_t row = row_of(a, b);
+  if (row < 0) return;
+  const int64_t L = clamp_len(a, a.seq_lens[row]);
   const int n_tiles = static_cast<int>(q3::cdiv(L, kTile));
-  const int n_parts = static_cast<int>(q3::cdiv(n_tiles, kTilesPerPart));
+  const int n_parts = static_cast<int>(q3::cdiv(n_tiles, kGridTilesPerPart));
   if (n_parts <= 1) return;
   const int64_t base = (static_cast<int64_t>(b) * a.Hq + hq) * a.max_parts;
+  const float* lse = a.ws_lse + base;
   float M = q3::kNegInf;
-  for (int p = 0; p < n_parts; ++p) M = fmaxf(M, a.ws_lse[base + p]);
+  for (int p0 = 0; p0 < n_parts; p0 += kBatch) {
+    float v[kBatch];
+#pragma unroll
+    for (int i = 0; i < kBatch; ++i) v[i] = p0 + i < n_parts ? lse[p0 + i] : q3::kNegInf;
+#pragma unroll
+    for (int i = 0; i < kBatch; ++i) M = fmaxf(M, v[i]);
+  }
   const float M_use = M == q3::kNegInf ? 0.f : M;
   float sw = 0.f, o = 0.f;
-  for (int p = 0; p < n_parts; ++p) {
-    const float w = q3::fast_exp2(a.ws_lse[base + p] - M_use);
-    sw += w;
-    o += w * a.ws_o[(base + p) * kD + d];
+  for (int p0 = 0; p0 < n_parts; p0 += kBatch) {
+    float wv[kBatch], ov[kBatch];
+#pragma unroll
+    for (int i = 0; i < kBatch; ++i) {
+      const bool ok = p0 + i < n_parts;
+      wv[i] = ok ? lse[p0 + i] : q3::kNegInf;
+      ov[i] = ok ? a.ws_o[(base + p0 + i) * kD + d] : 0.f;
+    }
+#pragma unroll
+    for (int i = 0; i < kBatch; ++i) {
+      const float wi = q3::fast_exp2(wv[i] - M_use);
+      sw += wi;
+      o += wi * ov[i];
+    }
   }
   o = sw > 0.f ? o / sw : 0.f;
   a.out[b * a.o_sb + static_cast<int64_t>(hq) * a.o_sh + d] = q3::bf16_bits(o);
 }
 
-constexpr int kTilesPerWave = 4;
-constexpr int kTilesPerPart = kTilesPerWave * kWaves;
+// ---------------------------------------------------------------------------
+// Host side.
 
-int64_t max_parts_for(int64_t max_pages, int block_size) {
-  const int64_t max_tiles = q3::cdiv(max_pages * block_size, kTile);
-  return q3::cdiv(max_tiles, kTilesPerPart);
+int cu_count() {
+  static int cached[64] = {0};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 0;
+  if (cached[dev] == 0) {
+    int n = 0;
+    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess)
+      return 0;
+    cached[dev] = n;
+  }
+  return cached[dev];
+}
+
+int64_t align256(int64_t x) { return (x + 255) / 256 * 256; }
+
+struct StreamLayout {
+  int64_t po, plse, pref, meta, total;
+};
+
+StreamLayout stream_layout(int B, int64_t waves) {
+  StreamLayout s;
+  s.po = 0;
+  s.plse = s.po + align256(waves * 2 * kMaxG * kD * 4);
+  s.pref = s.plse + align256(waves * 2 * kMaxG * 4);
+  s.meta = s.pref + align256((static_cast<int64_t>(B) + 1) * 4);
+  s.total = s.meta + 256;
+  return s;
+}
+
+int64_t grid_parts(int64_t max_pages, int block_size) {
+  return q3::cdiv(q3::cdiv(max_pages * block_size, kTile), kGridTilesPerPart);
+}
+
+int64_t grid_bytes(int B, int num_heads, int64_t max_pages, int block_size) {
+  const int64_t slots = static_cast<int64_t>(B) * num_heads * grid_parts(max_pages, block_size);
+  return align256(slots * kD * 4) + align256(slots * 4);
 }
 
 }  // namespace
@@ -323,11 +788,9 @@ extern "C" size_t qwen3_paged_decode_workspace_bytes(int B, int num_heads, int h
   if (B <= 0 || num_heads <= 0 || head_dim != kD || max_pages <= 0 || block_size <= 0 ||
       block_size % kTile != 0)
     return 0;
-  const int64_t parts = max_parts_for(max_pages, block_size);
-  const int64_t slots = static_cast<int64_t>(B) * num_heads * parts;
-  // ws_o (slots x D fp32) followed by ws_lse (slots fp32), 256-byte aligned.
-  const int64_t o_bytes = ((slots * kD * 4 + 255) / 256) * 256;
-  return static_cast<size_t>(o_bytes + ((slots * 4 + 255) / 256) * 256);
+  if (B <= kStreamMaxB)
+    return static_cast<size_t>(stream_layout(B, int64_t(kStreamMaxWgs) * kWaves).total);
+  return static_cast<size_t>(grid_bytes(B, num_heads, max_pages, block_size));
 }
 
 extern "C" int qwen3_paged_decode_bf16(
@@ -359,23 +822,26 @@ extern "C" int qwen3_paged_decode_bf16(
   if (B == 0) return QWEN3_OK;
   if (B > 65535 || num_kv_heads > 65535)
     return q3::fail(QWEN3_EINVAL, "%s: batch %d too large for one launch", who, B);
-  // 16-byte vector access of q/K/V rows and 4-byte stores of output pairs.
+  if (max_pages * block_size > (int64_t(1) << 30))
+    return q3::fail(QWEN3_EINVAL, "%s: max_pages * block_size too large", who);
+  // 16-byte vector access of q/K/V/out rows.
   const int64_t vec_strides[] = {q_strides[0], q_strides[1], k_strides[0], k_strides[1],
-                                 k_strides[2], v_strides[0], v_strides[1], v_strides[2]};
+                                 k_strides[2], v_strides[0], v_strides[1], v_strides[2],
+                                 out_strides[0], out_strides[1]};
   bool ok = q3::aligned16(q) && q3::aligned16(k_cache) && q3::aligned16(v_cache) &&
-            (reinterpret_cast<uintptr_t>(out) & 3u) == 0 && out_strides[0] % 2 == 0 &&
-            out_strides[1] % 2 == 0;
+            q3::aligned16(out);
   for (int64_t s : vec_strides) ok = ok && s % 8 == 0;
   if (!ok)
-    return q3::fail(QWEN3_EALIGN, "%s: q/K/V need 16-byte aligned rows (strides multiple "
-                    "of 8 elements), out needs 4-byte aligned element pairs", who);
-  const int64_t parts = max_parts_for(max_pages, block_size);
-  if (parts > 0x7fffffff) return q3::fail(QWEN3_EINVAL, "%s: max_pages too large", who);
+    return q3::fail(QWEN3_EALIGN, "%s: q/K/V/out need 16-byte aligned rows (strides multiple "
+                    "of 8 elements)", who);
   const size_t need = qwen3_paged_decode_workspace_bytes(B, num_heads, head_dim, max_pages,
                                                          block_size);
-  if (parts > 1 && (!workspace || workspace_bytes < need))
+  if (need == 0) return q3::fail(QWEN3_EINVAL, "%s: cannot size the workspace", who);
+  if (!workspace || workspace_bytes < need)
     return q3::fail(QWEN3_EWORKSPACE, "%s: workspace of %zu bytes needed, %zu given", who,
                     need, workspace ? workspace_bytes : (size_t)0);
+  if (!q3::aligned16(workspace))
+    return q3::fail(QWEN3_EALIGN, "%s: workspace must be 16-byte aligned", who);
 
   DecodeArgs a{};
   a.q = static_cast<const uint16_t*>(q);
@@ -406,22 +872,37 @@ extern "C" int qwen3_paged_decode_bf16(
   a.G = num_heads / num_kv_heads;
   a.bs = block_size;
   a.scale_log2 = scale * q3::kLog2e;
-  a.max_parts = static_cast<int>(parts);
-  if (parts > 1) {
-    const int64_t slots = static_cast<int64_t>(B) * num_heads * parts;
-    a.ws_o = static_cast<float*>(workspace);
-    a.ws_lse = reinterpret_cast<float*>(static_cast<char*>(workspace) +
-                                        ((slots * kD * 4 + 255) / 256) * 256);
-  }
+  char* ws = static_cast<char*>(workspace);
 
   q3::clear_error();
   hipStream_t s = static_cast<hipStream_t>(stream);
-  hipLaunchKernelGGL((paged_decode_part_kernel<kTilesPerWave>),
-                     dim3(static_cast<unsigned>(parts), num_kv_heads, B), dim3(kWaves * 64), 0,
-                     s, a);
+  if (B <= kStreamMaxB) {
+    int wgs = cu_count() * kStreamWgPerCu;
+    if (wgs <= 0) return q3::fail(QWEN3_EINVAL, "%s: cannot query the device's CU count", who);
+    wgs = wgs < kStreamMaxWgs ? wgs : kStreamMaxWgs;
+    const StreamLayout L = stream_layout(B, int64_t(kStreamMaxWgs) * kWaves);
+    a.s_po = reinterpret_cast<float*>(ws + L.po);
+    a.s_plse = reinterpret_cast<float*>(ws + L.plse);
+    a.s_pref = reinterpret_cast<int32_t*>(ws + L.pref);
+    a.s_meta = reinterpret_cast<int32_t*>(ws + L.meta);
+    hipLaunchKernelGGL(paged_decode_stream_kernel, dim3(wgs), dim3(kWaves * 64), 0, s, a);
+    int rc = q3::launch_status(who);
+    if (rc) return rc;
+    hipLaunchKernelGGL(paged_decode_stream_merge_kernel, dim3(num_kv_heads, B), dim3(64 * a.G),
+                       0, s, a);
+    return q3::launch_status(who);
+  }
+  const int64_t parts = grid_parts(max_pages, block_size);
+  if (parts > 0x7fffffff) return q3::fail(QWEN3_EINVAL, "%s: max_pages too large", who);
+  a.max_parts = static_cast<int>(parts);
+  const int64_t slots = static_cast<int64_t>(B) * num_heads * parts;
+  a.ws_o = reinterpret_cast<float*>(ws);
+  a.ws_lse = reinterpret_cast<float*>(ws + align256(slots * kD * 4));
+  const size_t lds = static_cast<size_t>(kWaves) * a.G * kOStride * sizeof(float);
+  hipLaunchKernelGGL(paged_decode_grid_kernel, dim3(static_cast<unsigned>(parts), num_kv_heads, B),
+                     dim3(kWaves * 64), lds, s, a);
   int rc = q3::launch_status(who);
   if (rc || parts == 1) return rc;
-  hipLaunchKernelGGL((paged_decode_reduce_kernel<kTilesPerWave>), dim3(num_heads, B), dim3(kD),
-                     0, s, a);
+  hipLaunchKernelGGL(paged_decode_grid_merge_kernel, dim3(num_heads, B), dim3(kD), 0, s, a);
   return q3::launch_status(who);
 }

@@ -34,11 +34,18 @@ def test_library_exports_every_declared_symbol():
 
 def test_workspace_bytes():
     lib = _lib.load()
-    # 256 batch x 32 heads x ceil(512 pages * 16 / 256) partitions x (128 + 1) fp32
-    parts = -(-512 * 16 // 256)
-    slots = 256 * 32 * parts
-    expect = -(-slots * 128 * 4 // 256) * 256 + -(-slots * 4 // 256) * 256
+    def a256(x):
+        return -(-x // 256) * 256
+
+    # batches up to 2048: two (128 + 1)-float partial slots per wave for up to
+    # 4096 waves x 16 query columns, plus the (B + 1)-entry tile prefix
+    waves = 4096
+    expect = a256(waves * 2 * 16 * 128 * 4) + a256(waves * 2 * 16 * 4) + a256(257 * 4) + 256
     assert lib.qwen3_paged_decode_workspace_bytes(256, 32, 128, 512, 16) == expect
+    # larger batches: one partial per (b, query head, 2048-token partition)
+    slots = 4096 * 32 * -(-512 * 16 // 2048)
+    assert lib.qwen3_paged_decode_workspace_bytes(4096, 32, 128, 512, 16) == \
+        a256(slots * 128 * 4) + a256(slots * 4)
     assert lib.qwen3_paged_decode_workspace_bytes(4, 16, 64, 64, 16) == 0  # head_dim 64 not built
     assert lib.qwen3_paged_decode_workspace_bytes(4, 16, 128, 64, 8) == 0  # block_size 8
 

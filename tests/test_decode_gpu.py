@@ -177,3 +177,44 @@ def make_device_decode(lens, hq, hkv, dev, seed=0, slack=0.1, block_size=16):
     sl = torch.tensor([L - 1 for L in lens], dtype=torch.int32, device=dev)
     rows = torch.arange(len(lens), dtype=torch.int32, device=dev)
     return dict(q=q, k=k, v=v, bt=bt, seq_lens=sl, row_ids=rows)
+
+
+def test_decode_stream_many_short_segments(gpu):
+    """Many short sequences per wave, empty contexts mixed in (bias 0): every
+    wave crosses several sequence-head boundaries and splits some."""
+    from qwen3_engine_from_scratch_amd.kernels.paged_attention import paged_attention_decode_hip
+
+    g = torch.Generator().manual_seed(21)
+    lens = [int(x) for x in torch.randint(0, 70, (700,), generator=g)]
+    lens[5] = lens[300] = 0
+    announce(f"decode stream many segments B={len(lens)}")
+    t = make_device_decode([max(L, 1) for L in lens], 16, 8, gpu, seed=3, slack=0.2)
+    t["seq_lens"] = torch.tensor(lens, dtype=torch.int32, device=gpu)  # bias 0: L = lens
+    out = paged_attention_decode_hip(t["q"], t["k"], t["v"], t["bt"], t["seq_lens"],
+                                     t["row_ids"], 16, seq_len_bias=0)
+    torch.cuda.synchronize()
+    nz = [b for b, L in enumerate(lens) if L > 0]
+    sel = torch.tensor(nz, device=gpu)
+    ref = gpu_dense_decode_fp32(t["q"][sel], t["k"], t["v"], t["bt"], t["seq_lens"],
+                                t["row_ids"][sel], 16, bias=0)
+    assert_close_attn(out[sel], ref, "many segments")
+    for b, L in enumerate(lens):
+        if L == 0:
+            assert not out[b].any()
+
+
+def test_decode_grid_path_large_batch(gpu):
+    """Batches above the stream path's table size use the grid kernel."""
+    from qwen3_engine_from_scratch_amd.kernels.paged_attention import paged_attention_decode_hip
+
+    g = torch.Generator().manual_seed(22)
+    lens = [int(x) for x in torch.randint(1, 3000, (2100,), generator=g)]
+    announce(f"decode grid path B={len(lens)}")
+    t = make_device_decode(lens, 32, 8, gpu, seed=4, slack=0.05)
+    out = paged_attention_decode_hip(t["q"], t["k"], t["v"], t["bt"], t["seq_lens"],
+                                     t["row_ids"], 16)
+    torch.cuda.synchronize()
+    sel = torch.arange(0, 2100, 37, device=gpu)
+    ref = gpu_dense_decode_fp32(t["q"][sel], t["k"], t["v"], t["bt"], t["seq_lens"],
+                                t["row_ids"][sel], 16)
+    assert_close_attn(out[sel], ref, "grid path")
