@@ -8,26 +8,39 @@
 //
 // Design (MI355X-first):
 //  * One 256-thread workgroup (4 wave64s) per (query tile, head group,
-//    sequence).  The head group holds HG query heads that share one KV
-//    head (HG = the largest of 4, 2, 1 dividing G), so a K/V tile staged in
-//    LDS serves every head of the group; each wave owns 32 query rows of one
-//    head, and the tile covers 32 * 4 / HG rows.
-//  * Query tiles are dispatched heaviest-first (the causal row tile with the
-//    most keys is launched first) to shorten the ragged tail.
-//  * Scores are computed transposed, S^T(32 keys x 32 queries) = K Q^T, with
-//    mfma_f32_32x32x16_bf16, so each lane owns one query column and 16 of its
-//    keys: the row max/sum needs one cross-lane step, and the S^T register
+//    sequence).  The head group holds HG query heads that share one KV head
+//    (HG = the largest of 4, 2, 1 dividing G), so a K/V tile staged in LDS
+//    serves every head of the group; each wave owns 32 query rows of one
+//    head.  Query tiles are dispatched heaviest-first (the causal row tile
+//    with the most keys first) to shorten the ragged tail.  Two workgroups
+//    share a CU (two waves per SIMD), so one wave's softmax overlaps the
+//    other's matrix-core work.
+//  * K/V tiles of 64 keys are double-buffered in LDS: the next tile's global
+//    loads are issued before the current tile's math and land in the other
+//    buffer after it, with a single barrier per tile.
+//  * Scores are computed transposed, S^T(32 keys x 32 queries) = K Q^T with
+//    mfma_f32_32x32x16_bf16: each lane owns one query column and 16 of its
+//    keys, so the row max needs one cross-lane step, and the S^T register
 //    layout is directly the B operand (P^T) of O^T = V^T P^T.
-//  * The V^T A-operand is assembled in-lane from 8-byte LDS reads of V rows
-//    with byte permutes.  Causal blocks above the diagonal are skipped.
+//  * V is staged into LDS transposed (V^T, one row per dim), once per
+//    workgroup, with the keys of each 16-key chunk stored in the order the
+//    P^T operand holds them, so each PV A operand is one 16-byte LDS read.
+//  * Softmax in the exp2 domain with the scale folded into one FMA; the
+//    running max is only raised (and the accumulator rescaled) when a new
+//    score exceeds it by more than 2^8, which keeps every P <= 256 and makes
+//    rescales rare; masking runs only on diagonal and tail tiles.
 #include "common.hpp"
 
 namespace {
 
 constexpr int kD = 128;
-constexpr int kBN = 64;             // keys per staged K/V tile
-constexpr int kLds = kD + 8;        // padded LDS row (elements)
+constexpr int kBN = 64;              // keys per staged K/V tile
+constexpr int kKStride = kD + 8;     // K tile row (elements), padded
+constexpr int kVtStride = kBN + 8;   // V^T tile row (elements), padded
 constexpr int kWaves = 4;
+constexpr float kRescaleSlack = 8.f; // log2 headroom before the max is raised
+constexpr int kMaxSeqs = 256;         // persistent path: sequences ranked in LDS
+constexpr int kScanMax = 1024;        // persistent path: query-tile ranks in LDS
 
 struct PrefillArgs {
   const uint16_t* q;
@@ -42,16 +55,75 @@ struct PrefillArgs {
   int num_seqs;
   int64_t total;
   int Hq, G, HG;
+  int groups;    // query-head groups (Hq / HG)
   int rows;      // query rows per head per workgroup (32 * kWaves / HG)
   int n_mtiles;  // grid.z
   float scale_log2;
   int causal;
 };
 
-__global__ __launch_bounds__(kWaves * 64) void varlen_prefill_kernel(PrefillArgs a) {
-  const int seq = blockIdx.x;
-  const int hg = blockIdx.y;
-  const int mt = a.n_mtiles - 1 - static_cast<int>(blockIdx.z);  // heaviest first
+// Position of key `key` (0..63) of a tile inside its V^T row: within each
+// 16-key chunk the P^T operand of lane half hl holds keys
+// {8a + 4hl + e : a, e}, stored contiguously at 8hl + 4a + e.
+__device__ __forceinline__ int vt_pos(int key) {
+  const int kc = key >> 4, a = (key >> 3) & 1, hl = (key >> 2) & 1, e = key & 3;
+  return 16 * kc + 8 * hl + 4 * a + e;
+}
+
+struct Staged {
+  q3::u32x4 k[4];  // K rows of this thread (16 bytes each)
+  q3::u32x4 v[4];  // V of keys 4*kg + i, dims 8*dg .. +7
+};
+
+__device__ __forceinline__ void stage_load(Staged& st, const PrefillArgs& a, int64_t start,
+                                           int len, int kvh, int n0, int tid) {
+  const q3::u32x4 z = {0u, 0u, 0u, 0u};
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int idx = tid + i * kWaves * 64;
+    const int r = idx >> 4;
+    const int c8 = (idx & 15) * 8;
+    st.k[i] = z;
+    if (n0 + r < len)
+      st.k[i] = q3::ld16(a.k + (start + n0 + r) * a.k_st + static_cast<int64_t>(kvh) * a.k_sh + c8);
+  }
+  const int dg = tid >> 4, kg = tid & 15;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int key = 4 * kg + i;
+    st.v[i] = z;
+    if (n0 + key < len)
+      st.v[i] = q3::ld16(a.v + (start + n0 + key) * a.v_st + static_cast<int64_t>(kvh) * a.v_sh +
+                         8 * dg);
+  }
+}
+
+__device__ __forceinline__ void stage_store(const Staged& st, uint16_t* s_k, uint16_t* s_vt,
+                                            int tid) {
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int idx = tid + i * kWaves * 64;
+    const int r = idx >> 4;
+    const int c8 = (idx & 15) * 8;
+    *reinterpret_cast<q3::u32x4*>(&s_k[r * kKStride + c8]) = st.k[i];
+  }
+  // Transpose the 4 keys x 8 dims block: dim 8*dg + j gets keys 4*kg .. +3.
+  const int dg = tid >> 4, kg = tid & 15;
+  const int pos = vt_pos(4 * kg);
+#pragma unroll
+  for (int j = 0; j < 8; ++j) {
+    const int w = j >> 1, h = j & 1;
+    q3::u32x2 col = {q3::pick_halves(st.v[0][w], st.v[1][w], h),
+                     q3::pick_halves(st.v[2][w], st.v[3][w], h)};
+    *reinterpret_cast<q3::u32x2*>(&s_vt[(8 * dg + j) * kVtStride + pos]) = col;
+  }
+}
+
+// One work item: query tile mt of sequence seq for head group hg.  Every
+// thread of the workgroup calls it; s_k / s_vt are the two LDS tile buffers.
+__device__ __forceinline__ void prefill_item(const PrefillArgs& a, int seq, int hg, int mt,
+                                             uint16_t (*s_k)[kBN * kKStride],
+                                             uint16_t (*s_vt)[kD * kVtStride]) {
   const int64_t start = a.cu[seq];
   const int64_t end = a.cu[seq + 1];
   if (start < 0 || end > a.total || end <= start) return;
@@ -70,92 +142,95 @@ __global__ __launch_bounds__(kWaves * 64) void varlen_prefill_kernel(PrefillArgs
   const int q0 = m0 + (wave % wph) * 32;  // first query row of this wave
   const int qrow = q0 + l32;               // the query column this lane owns
 
-  __shared__ uint16_t s_k[kBN * kLds];
-  __shared__ uint16_t s_v[kBN * kLds];
+  const int kend = a.causal ? min(len, m0 + a.rows) : len;
+  const int n_tiles = (kend + kBN - 1) / kBN;
+
+  Staged stg;
+  stage_load(stg, a, start, len, kvh, 0, tid);
 
   // Q^T as the B operand: lane (query l32, k-group hl), chunk c: dims
   // c*16 + 8*hl .. +7.
   q3::bf16x8 qv[8];
   {
+    const q3::u32x4 z = {0u, 0u, 0u, 0u};
     const bool ok = qrow < len;
-    const uint16_t* qp = a.q + (start + qrow) * a.q_st + static_cast<int64_t>(head) * a.q_sh + 8 * hl;
+    const uint16_t* qp =
+        a.q + (start + (ok ? qrow : 0)) * a.q_st + static_cast<int64_t>(head) * a.q_sh + 8 * hl;
 #pragma unroll
-    for (int c = 0; c < 8; ++c) {
-      q3::u32x4 z = {0u, 0u, 0u, 0u};
-      qv[c] = q3::as_bf16x8(ok ? q3::ld16(qp + c * 16) : z);
-    }
+    for (int c = 0; c < 8; ++c) qv[c] = q3::as_bf16x8(ok ? q3::ld16(qp + c * 16) : z);
   }
 
-  float m_run = q3::kNegInf;
-  float l_run = 0.f;
-  q3::f32x16 acc[4];  // acc[db][r] = O[qrow][4*(8*(r/4) + 4*hl + r%4) + db]
+  stage_store(stg, s_k[0], s_vt[0], tid);
+  __syncthreads();
+
+  float m_run = q3::kNegInf;  // running max (log2 domain) of this query
+  float l_run = 0.f;          // this lane's share of the denominator
+  q3::f32x16 acc[4];          // acc[db][r] = O[qrow][32*db + 8*(r/4) + 4*hl + r%4]
 #pragma unroll
   for (int db = 0; db < 4; ++db)
 #pragma unroll
     for (int r = 0; r < 16; ++r) acc[db][r] = 0.f;
 
-  const int kend = a.causal ? min(len, m0 + a.rows) : len;
-  const int wave_last_q = min(q0 + 31, len - 1);
   const bool wave_active = q0 < len;
+  const int wave_last_q = min(q0 + 31, len - 1);
+  const float c = a.scale_log2;
 
-  for (int n0 = 0; n0 < kend; n0 += kBN) {
-    // ---- stage K and V rows [n0, n0 + kBN) of KV head kvh into LDS ----
-#pragma unroll
-    for (int i = 0; i < (kBN * kD / 8) / (kWaves * 64); ++i) {
-      const int idx = tid + i * kWaves * 64;
-      const int r = idx / (kD / 8);
-      const int c8 = (idx % (kD / 8)) * 8;
-      q3::u32x4 kx = {0u, 0u, 0u, 0u}, vx = {0u, 0u, 0u, 0u};
-      if (n0 + r < len) {
-        const int64_t t = start + n0 + r;
-        kx = q3::ld16(a.k + t * a.k_st + static_cast<int64_t>(kvh) * a.k_sh + c8);
-        vx = q3::ld16(a.v + t * a.v_st + static_cast<int64_t>(kvh) * a.v_sh + c8);
-      }
-      *reinterpret_cast<q3::u32x4*>(&s_k[r * kLds + c8]) = kx;
-      *reinterpret_cast<q3::u32x4*>(&s_v[r * kLds + c8]) = vx;
-    }
-    __syncthreads();
+  for (int it = 0; it < n_tiles; ++it) {
+    const int n0 = it * kBN;
+    const int buf = it & 1;
+    const bool more = it + 1 < n_tiles;
+    if (more) stage_load(stg, a, start, len, kvh, n0 + kBN, tid);
 
     // Causal: the tile is entirely above this wave's last query row.
     const bool wave_skip = !wave_active || (a.causal && n0 > wave_last_q);
     if (!wave_skip) {
+      const uint16_t* kt = s_k[buf];
+      const uint16_t* vt = s_vt[buf];
       // ---- S^T = K Q^T for two 32-key blocks ----
       q3::f32x16 s[2];
 #pragma unroll
       for (int kb = 0; kb < 2; ++kb) {
 #pragma unroll
         for (int r = 0; r < 16; ++r) s[kb][r] = 0.f;
-        const uint16_t* kp = &s_k[(kb * 32 + l32) * kLds + 8 * hl];
+        const uint16_t* kp = kt + (kb * 32 + l32) * kKStride + 8 * hl;
 #pragma unroll
-        for (int c = 0; c < 8; ++c) {
-          const q3::bf16x8 kf = q3::as_bf16x8(*reinterpret_cast<const q3::u32x4*>(kp + c * 16));
-          s[kb] = q3::mfma32x32x16(kf, qv[c], s[kb]);
+        for (int cc = 0; cc < 8; ++cc) {
+          const q3::bf16x8 kf = q3::as_bf16x8(*reinterpret_cast<const q3::u32x4*>(kp + cc * 16));
+          s[kb] = q3::mfma32x32x16(kf, qv[cc], s[kb]);
         }
       }
-      // ---- scale, mask, running max ----
+      // ---- mask (diagonal / tail tiles only) and block max ----
       const bool need_mask = (n0 + kBN > len) || (a.causal && n0 + kBN - 1 > q0);
-      float mx = q3::kNegInf;
+      if (need_mask) {
+#pragma unroll
+        for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+          for (int r = 0; r < 16; ++r) {
+            const int key = n0 + kb * 32 + 8 * (r / 4) + 4 * hl + (r % 4);
+            const bool valid = key < len && (!a.causal || key <= qrow);
+            s[kb][r] = valid ? s[kb][r] : q3::kNegInf;
+          }
+      }
+      float bm = q3::kNegInf;
 #pragma unroll
       for (int kb = 0; kb < 2; ++kb)
 #pragma unroll
-        for (int r = 0; r < 16; ++r) {
-          float x = s[kb][r] * a.scale_log2;
-          if (need_mask) {
-            const int key = n0 + kb * 32 + 8 * (r / 4) + 4 * hl + (r % 4);
-            const bool valid = key < len && (!a.causal || key <= qrow);
-            x = valid ? x : q3::kNegInf;
-          }
-          s[kb][r] = x;
-          mx = fmaxf(mx, x);
-        }
-      mx = fmaxf(mx, q3::shfl_xor(mx, 32));
-      const float m_new = fmaxf(m_run, mx);
-      const float m_use = m_new == q3::kNegInf ? 0.f : m_new;
-      const float alpha = q3::fast_exp2(m_run - m_use);
-      m_run = m_new;
-      float psum = 0.f;
-      // P^T as B operands: chunk (kb, kc) takes registers 8*kc .. 8*kc+7.
+        for (int r = 0; r < 16; r += 2) bm = fmaxf(bm, fmaxf(s[kb][r], s[kb][r + 1]));
+      bm = fmaxf(bm, q3::shfl_xor(bm, 32));
+      const float m_cand = bm * c;
+      const bool raise = m_cand > m_run + kRescaleSlack;
+      if (__any(raise)) {
+        const float m_new = raise ? m_cand : m_run;
+        const float alpha = raise ? q3::fast_exp2(m_run - m_new) : 1.f;
+        m_run = m_new;
+        l_run *= alpha;
+#pragma unroll
+        for (int db = 0; db < 4; ++db) acc[db] *= alpha;
+      }
+      const float m_use = m_run == q3::kNegInf ? 0.f : m_run;
+      // ---- P = exp2(s * c - m), P^T as B operands (registers 8*kc .. +7) ----
       q3::bf16x8 p[2][2];
+      float psum = 0.f;
 #pragma unroll
       for (int kb = 0; kb < 2; ++kb)
 #pragma unroll
@@ -163,41 +238,29 @@ __global__ __launch_bounds__(kWaves * 64) void varlen_prefill_kernel(PrefillArgs
           float e[8];
 #pragma unroll
           for (int i = 0; i < 8; ++i) {
-            e[i] = q3::fast_exp2(s[kb][8 * kc + i] - m_use);
+            e[i] = q3::fast_exp2(__builtin_fmaf(s[kb][8 * kc + i], c, -m_use));
             psum += e[i];
           }
           q3::u32x4 pk = {q3::pack_bf16x2(e[0], e[1]), q3::pack_bf16x2(e[2], e[3]),
                           q3::pack_bf16x2(e[4], e[5]), q3::pack_bf16x2(e[6], e[7])};
           p[kb][kc] = q3::as_bf16x8(pk);
         }
-      l_run = l_run * alpha + psum;
-#pragma unroll
-      for (int db = 0; db < 4; ++db) acc[db] *= alpha;
-
-      // ---- O^T += V^T P^T ----
-      // Chunk (kb, kc), element e pairs with key kb*32 + 16*kc + 8*(e/4) +
-      // 4*hl + e%4; the A operand of dim block db is V[key][4*l32 + db].
+      l_run += psum;
+      // ---- O^T += V^T P^T: chunk KC = 2*kb + kc of 16 keys ----
 #pragma unroll
       for (int kb = 0; kb < 2; ++kb)
 #pragma unroll
         for (int kc = 0; kc < 2; ++kc) {
-          q3::u32x2 vr[8];
-#pragma unroll
-          for (int e = 0; e < 8; ++e) {
-            const int key = kb * 32 + 16 * kc + 8 * (e / 4) + 4 * hl + (e % 4);
-            vr[e] = *reinterpret_cast<const q3::u32x2*>(&s_v[key * kLds + 4 * l32]);
-          }
+          const int KC = 2 * kb + kc;
 #pragma unroll
           for (int db = 0; db < 4; ++db) {
-            const int w = db >> 1, h = db & 1;
-            q3::u32x4 av = {q3::pick_halves(vr[0][w], vr[1][w], h),
-                            q3::pick_halves(vr[2][w], vr[3][w], h),
-                            q3::pick_halves(vr[4][w], vr[5][w], h),
-                            q3::pick_halves(vr[6][w], vr[7][w], h)};
-            acc[db] = q3::mfma32x32x16(q3::as_bf16x8(av), p[kb][kc], acc[db]);
+            const q3::bf16x8 vf = q3::as_bf16x8(*reinterpret_cast<const q3::u32x4*>(
+                vt + (32 * db + l32) * kVtStride + 16 * KC + 8 * hl));
+            acc[db] = q3::mfma32x32x16(vf, p[kb][kc], acc[db]);
           }
         }
     }
+    if (more) stage_store(stg, s_k[buf ^ 1], s_vt[buf ^ 1], tid);
     __syncthreads();
   }
 
@@ -206,11 +269,139 @@ __global__ __launch_bounds__(kWaves * 64) void varlen_prefill_kernel(PrefillArgs
   const float inv = l_run > 0.f ? 1.f / l_run : 0.f;
   uint16_t* op = a.o + (start + qrow) * a.o_st + static_cast<int64_t>(head) * a.o_sh;
 #pragma unroll
-  for (int r = 0; r < 16; ++r) {
-    const int i = 8 * (r / 4) + 4 * hl + (r % 4);
-    q3::u32x2 w = {q3::pack_bf16x2(acc[0][r] * inv, acc[1][r] * inv),
-                   q3::pack_bf16x2(acc[2][r] * inv, acc[3][r] * inv)};
-    *reinterpret_cast<q3::u32x2*>(op + 4 * i) = w;
+  for (int db = 0; db < 4; ++db)
+#pragma unroll
+    for (int g4 = 0; g4 < 4; ++g4) {
+      const int d = 32 * db + 8 * g4 + 4 * hl;
+      q3::u32x2 w = {q3::pack_bf16x2(acc[db][4 * g4] * inv, acc[db][4 * g4 + 1] * inv),
+                     q3::pack_bf16x2(acc[db][4 * g4 + 2] * inv, acc[db][4 * g4 + 3] * inv)};
+      *reinterpret_cast<q3::u32x2*>(op + d) = w;
+    }
+}
+
+
+// Flat grid (fallback for many sequences / very long ones): one workgroup
+// per virtual item, head group fastest so consecutive workgroups go to
+// different XCDs and all items of one KV head share an XCD's L2; query tiles
+// heaviest first.  Items past a sequence's end exit at once.
+__global__ __launch_bounds__(kWaves * 64) __attribute__((amdgpu_waves_per_eu(2, 2)))
+void varlen_prefill_flat_kernel(PrefillArgs a) {
+  __shared__ uint16_t s_k[2][kBN * kKStride];
+  __shared__ uint16_t s_vt[2][kD * kVtStride];
+  const int64_t id = blockIdx.x;
+  const int hg = static_cast<int>(id % a.groups);
+  const int seq = static_cast<int>((id / a.groups) % a.num_seqs);
+  const int mt =
+      a.n_mtiles - 1 - static_cast<int>(id / (static_cast<int64_t>(a.groups) * a.num_seqs));
+  prefill_item(a, seq, hg, mt, s_k, s_vt);
+}
+
+// Exclusive prefix sum over n <= kScanMax ints held in LDS (in place); returns
+// the total.  Called by all threads of the workgroup.
+__device__ __forceinline__ int block_exclusive_scan(int* v, int n, int* s_wsum) {
+  constexpr int kPer = kScanMax / (kWaves * 64);
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  int local[kPer];
+  int sum = 0;
+#pragma unroll
+  for (int i = 0; i < kPer; ++i) {
+    const int j = tid * kPer + i;
+    local[i] = j < n ? v[j] : 0;
+    sum += local[i];
+  }
+  int incl = sum;
+#pragma unroll
+  for (int o = 1; o < 64; o <<= 1) {
+    const int y = __shfl_up(incl, o, 64);
+    if (lane >= o) incl += y;
+  }
+  if (lane == 63) s_wsum[wave] = incl;
+  __syncthreads();
+  int run = incl - sum, total = 0;
+#pragma unroll
+  for (int w = 0; w < kWaves; ++w) {
+    if (w < wave) run += s_wsum[w];
+    total += s_wsum[w];
+  }
+#pragma unroll
+  for (int i = 0; i < kPer; ++i) {
+    const int j = tid * kPer + i;
+    if (j < n) v[j] = run;
+    run += local[i];
+  }
+  __syncthreads();
+  return total;
+}
+
+// Persistent grid (two workgroups per CU).  Every workgroup builds the same
+// compact list of non-empty items ordered heaviest first (query tiles of the
+// highest index first; within one, longest sequences first, head group
+// fastest) and takes its share in a snake order over rounds, which balances
+// the causal work per CU without atomics.  The snake mirrors whole groups of
+// 8 positions so an item's head group keeps mapping to the same XCD.
+#ifndef Q3_PREFILL_PERSISTENT_WAVES_PER_EU
+#define Q3_PREFILL_PERSISTENT_WAVES_PER_EU 2
+#endif
+__global__ __launch_bounds__(kWaves * 64)
+__attribute__((amdgpu_waves_per_eu(Q3_PREFILL_PERSISTENT_WAVES_PER_EU, Q3_PREFILL_PERSISTENT_WAVES_PER_EU)))
+void varlen_prefill_persistent_kernel(PrefillArgs a) {
+  __shared__ uint16_t s_k[2][kBN * kKStride];
+  __shared__ uint16_t s_vt[2][kD * kVtStride];
+  __shared__ int s_len[kMaxSeqs];
+  __shared__ int s_sorted[kMaxSeqs];
+  __shared__ int s_first[kScanMax];  // items before m-tile rank r (r = n_mtiles-1-mt)
+  __shared__ int s_wsum[kWaves];
+  const int tid = threadIdx.x;
+  const int S = a.num_seqs;
+  const int nm = a.n_mtiles;
+
+  for (int t = tid; t < S; t += kWaves * 64) {
+    const int64_t s0 = a.cu[t], s1 = a.cu[t + 1];
+    const bool ok = s0 >= 0 && s1 <= a.total && s1 > s0;
+    s_len[t] = ok ? static_cast<int>(s1 - s0) : 0;
+  }
+  __syncthreads();
+  // Rank by length, longest first (ties by index).
+  for (int t = tid; t < S; t += kWaves * 64) {
+    const int lt = s_len[t];
+    int rank = 0;
+    for (int u = 0; u < S; ++u) {
+      const int lu = s_len[u];
+      rank += (lu > lt || (lu == lt && u < t)) ? 1 : 0;
+    }
+    s_sorted[rank] = t;
+  }
+  __syncthreads();
+  // Items of m-tile rank r: groups x (number of sequences longer than mt*rows).
+  for (int r = tid; r < nm; r += kWaves * 64) {
+    const int mt = nm - 1 - r;
+    const int64_t thr = static_cast<int64_t>(mt) * a.rows;
+    int lo = 0, hi = S;  // first sorted index with len <= thr
+    while (lo < hi) {
+      const int mid = (lo + hi) >> 1;
+      if (s_len[s_sorted[mid]] > thr) lo = mid + 1; else hi = mid;
+    }
+    s_first[r] = lo * a.groups;
+  }
+  __syncthreads();
+  const int T = block_exclusive_scan(s_first, nm, s_wsum);
+
+  const int W = gridDim.x;
+  const int w = blockIdx.x;
+  const int w_mirror = (W / 8 - 1 - w / 8) * 8 + w % 8;
+  for (int round = 0;; ++round) {
+    const int64_t i = static_cast<int64_t>(round) * W + ((round & 1) ? w_mirror : w);
+    if (i >= T) break;
+    int lo = 0, hi = nm - 1;  // largest rank r with s_first[r] <= i
+    while (lo < hi) {
+      const int mid = (lo + hi + 1) >> 1;
+      if (s_first[mid] <= i) lo = mid; else hi = mid - 1;
+    }
+    const int j = static_cast<int>(i - s_first[lo]);
+    const int seq = s_sorted[j / a.groups];
+    const int hg = j % a.groups;
+    __syncthreads();  // the previous item's LDS tiles are no longer read
+    prefill_item(a, seq, hg, nm - 1 - lo, s_k, s_vt);
   }
 }
 
@@ -237,8 +428,6 @@ extern "C" int qwen3_varlen_prefill_bf16(const void* q, const int64_t q_strides[
   if (num_seqs < 0 || max_seqlen < 0 || total_tokens < 0)
     return q3::fail(QWEN3_EINVAL, "%s: bad sizes", who);
   if (num_seqs == 0 || max_seqlen == 0 || total_tokens == 0) return QWEN3_OK;
-  if (num_seqs > 0x7fffffff)
-    return q3::fail(QWEN3_EINVAL, "%s: too many sequences", who);
   const int64_t vec_strides[] = {q_strides[0], q_strides[1], k_strides[0], k_strides[1],
                                  v_strides[0], v_strides[1], o_strides[0], o_strides[1]};
   bool ok = q3::aligned16(q) && q3::aligned16(k) && q3::aligned16(v) && q3::aligned16(o);
@@ -270,13 +459,29 @@ extern "C" int qwen3_varlen_prefill_bf16(const void* q, const int64_t q_strides[
   a.n_mtiles = static_cast<int>(q3::cdiv(max_seqlen, a.rows));
   a.scale_log2 = scale * q3::kLog2e;
   a.causal = causal ? 1 : 0;
-  const int groups = num_heads / a.HG;
-  if (groups > 65535 || a.n_mtiles > 65535)
-    return q3::fail(QWEN3_EINVAL, "%s: grid too large (heads %d, max_seqlen %d)", who,
-                    num_heads, max_seqlen);
+  a.groups = num_heads / a.HG;
+  const int64_t blocks = static_cast<int64_t>(a.groups) * num_seqs * a.n_mtiles;
+  if (blocks > 0x7fffffff)
+    return q3::fail(QWEN3_EINVAL, "%s: grid too large (heads %d, seqs %d, max_seqlen %d)", who,
+                    num_heads, num_seqs, max_seqlen);
 
   q3::clear_error();
-  hipLaunchKernelGGL(varlen_prefill_kernel, dim3(num_seqs, groups, a.n_mtiles),
-                     dim3(kWaves * 64), 0, static_cast<hipStream_t>(stream), a);
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  int dev = 0, cus = 0, per_cu = 0;
+  // The persistent grid is exactly what stays resident: CUs x workgroups per CU.
+  const bool persistent =
+      num_seqs <= kMaxSeqs && a.n_mtiles <= kScanMax && hipGetDevice(&dev) == hipSuccess &&
+      hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess &&
+      hipOccupancyMaxActiveBlocksPerMultiprocessor(
+          &per_cu, reinterpret_cast<const void*>(varlen_prefill_persistent_kernel), kWaves * 64,
+          0) == hipSuccess &&
+      cus > 0 && per_cu > 0;
+  if (persistent) {
+    const int wgs = ((cus * per_cu + 7) / 8) * 8;  // multiple of 8 for the XCD-preserving snake
+    hipLaunchKernelGGL(varlen_prefill_persistent_kernel, dim3(wgs), dim3(kWaves * 64), 0, s, a);
+  } else {
+    hipLaunchKernelGGL(varlen_prefill_flat_kernel, dim3(static_cast<unsigned>(blocks)),
+                       dim3(kWaves * 64), 0, s, a);
+  }
   return q3::launch_status(who);
 }
