@@ -28,6 +28,7 @@ import json
 import os
 import sys
 import time
+from pathlib import Path
 
 HBM_PEAK_GBS = 8000.0
 MFMA_BF16_PEAK_TFLOPS = 2500.0
@@ -156,6 +157,22 @@ def cpu_baseline_decode(res, n_seq=64):
                       f"{dt:.2f} s"}
 
 
+PROFILE_DIR = Path(__file__).resolve().parent / "profiles"
+TRAFFIC_PROFILE = "paged_decode_stream_b256_qwen3_8b.md"
+
+
+def profiled_traffic(name: str):
+    """HBM bytes per launch measured offline with rocprofv3 --pmc FETCH_SIZE /
+    WRITE_SIZE (scaled by a known-size copy) and recorded in profiles/<name>."""
+    f = PROFILE_DIR / name
+    if not f.exists():
+        return None
+    for line in f.read_text().splitlines():
+        if line.startswith("traffic_bytes_per_launch:"):
+            return int(float(line.split(":", 1)[1]))
+    return None
+
+
 def bench_prefill(args, dev):
     import torch
 
@@ -213,6 +230,11 @@ def main(argv=None):
     ap.add_argument("--only", choices=["decode", "prefill"], default=None)
     ap.add_argument("--workload", choices=["config3", "config4"], default="config3")
     ap.add_argument("--cpu-sample", type=int, default=64, help="sequences in the CPU baseline sample")
+    ap.add_argument("--no-long-context", action="store_true",
+                    help="skip the secondary long-context (B=8, up to 128k tokens) decode line")
+    ap.add_argument("--calibrate-copy", action="store_true",
+                    help="also run a plain 1 GiB device copy (the known-size reference for "
+                         "rocprofv3 FETCH_SIZE / WRITE_SIZE counters)")
     args = ap.parse_args(argv)
     if args.gpus != 1:
         print(f"bench.py measures one GPU only: this build has no multi-GPU path "
@@ -227,6 +249,14 @@ def main(argv=None):
 
     _lib.load()
     dev = torch.device("cuda:0")
+    if args.calibrate_copy:
+        src = torch.ones(1 << 29, dtype=torch.bfloat16, device=dev)  # 1 GiB
+        dst = torch.empty_like(src)
+        for _ in range(3):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        del src, dst
+        torch.cuda.empty_cache()
     line = {"metric": METRIC, "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
             "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "bf16",
             "data": "synthetic (seeded N(0,1) q/K/V, seeded lengths and block tables)"}
@@ -239,13 +269,27 @@ def main(argv=None):
                           "block 16, pool 1.1x pages, random-permutation block tables",
                           "batch": len(res["lens"]), "sum_context_tokens": sum(res["lens"]),
                           "bytes_per_step": res["bytes"]}
+        traffic = profiled_traffic(TRAFFIC_PROFILE) if args.workload == "config3" else None
         line["roofline"] = {"bound": "hbm", "achieved": round(ach, 1), "peak": HBM_PEAK_GBS,
                             "unit": "GB/s", "frac": round(ach / HBM_PEAK_GBS, 4),
-                            "traffic": None, "kernel_ms": round(res["evt_ms"], 5)}
+                            "traffic": traffic, "kernel_ms": round(res["evt_ms"], 5),
+                            "kernel": "paged_decode_stream_kernel + paged_decode_stream_merge_kernel "
+                                      "(one decode call), HIP events on the launch stream",
+                            "traffic_source": f"profiles/{TRAFFIC_PROFILE}" if traffic else None}
         if not args.no_cpu_baseline:
             line["cpu_baseline"] = cpu_baseline_decode(res, args.cpu_sample)
         del res
         torch.cuda.empty_cache()
+        if args.workload == "config3" and not args.no_long_context:
+            long_args = argparse.Namespace(**{**vars(args), "workload": "config4"})
+            r4 = bench_decode(long_args, dev)
+            line["decode_long_context"] = {
+                "workload": r4["wname"] + ", 32 q / 8 kv heads, head_dim 128, bf16, block 16",
+                "value": round(r4["bytes"] / (r4["evt_ms"] * 1e-3) / 1e9, 1), "unit": "GB/s",
+                "ms_per_step": round(r4["evt_ms"], 5), "bytes_per_step": r4["bytes"],
+                "frac_hbm_peak": round(r4["bytes"] / (r4["evt_ms"] * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)}
+            del r4
+            torch.cuda.empty_cache()
     if args.only != "decode":
         pf = bench_prefill(args, dev)
         if args.only == "prefill":

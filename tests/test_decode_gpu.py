@@ -218,3 +218,15 @@ def test_decode_grid_path_large_batch(gpu):
     ref = gpu_dense_decode_fp32(t["q"][sel], t["k"], t["v"], t["bt"], t["seq_lens"],
                                 t["row_ids"][sel], 16)
     assert_close_attn(out[sel], ref, "grid path")
+
+
+def test_decode_config1_golden_fixture(gpu):
+    from pathlib import Path
+
+    f = np.load(Path(__file__).resolve().parent / "golden" / "decode_config1.npz", allow_pickle=False)
+    case = oi.config1_decode()
+    assert case.fingerprint() == str(f["sha256"])
+    announce("decode config1 vs golden fixture")
+    out, _ = _run(case, gpu)
+    assert_close_attn(out, torch.from_numpy(f["dense_fp64"]), "golden fp64")
+    assert_close_attn(out, torch.from_numpy(f["oracle_fp32"]), "golden oracle")

@@ -141,3 +141,28 @@ def test_unaligned_rows_use_element_path(gpu):
     update_kv_batch_hip(k_new, v_new, kb, vb, seq_lens.to(gpu), bt.to(gpu), rows.to(gpu), 0)
     torch.cuda.synchronize()
     assert np.array_equal(_u16(kb), ek) and np.array_equal(_u16(vb), ev)
+
+
+def test_slot_write_golden_fixture(gpu):
+    from pathlib import Path
+
+    from oracle import inputs as oi
+    from qwen3_engine_from_scratch_amd import _lib
+
+    f = np.load(Path(__file__).resolve().parent / "golden" / "slot_write.npz", allow_pickle=False)
+    c = oi.make_prefill_case([40, 23], 16, 8, 128, seed=4)
+    assert c.fingerprint() == str(f["sha256"])
+    kb = torch.zeros(c.num_blocks + 2, 3, 8, 16, 128, dtype=torch.bfloat16, device=gpu)
+    vb = torch.zeros_like(kb)
+    k, v, sm = c.k.to(gpu), c.v.to(gpu), c.slot_mapping.to(gpu)
+    announce("slot write vs golden fixture")
+    rc = _lib.load().qwen3_kv_write_slots_bf16(
+        k.data_ptr(), _lib.strides(k, (0, 1)), v.data_ptr(), _lib.strides(v, (0, 1)),
+        kb.data_ptr(), _lib.strides(kb, (0, 1, 2, 3)), vb.data_ptr(), _lib.strides(vb, (0, 1, 2, 3)),
+        kb.shape[0], 1, sm.data_ptr(), sm.numel(), 8, 128, 16, _lib.stream_of(gpu))
+    _lib.check(rc, "slots")
+    torch.cuda.synchronize()
+    ku, vu = _u16(kb), _u16(vb)
+    assert np.uint64(ku.astype(np.uint64).sum()) == f["k_checksum"]
+    assert np.uint64(vu.astype(np.uint64).sum()) == f["v_checksum"]
+    assert np.array_equal(np.argwhere(ku.any(axis=(2, 4))), f["touched"])

@@ -93,3 +93,18 @@ def test_prefill_batched_adaptor_pads_zero(gpu):
         s0 = int(c.cu_seqlens[b])
         assert_close_attn(out[b, :L], ref[s0:s0 + L], f"row {b}")
         assert not out[b, L:].any()
+
+
+def test_prefill_golden_fixture(gpu):
+    from pathlib import Path
+
+    import numpy as np
+    from tests_golden_params import PREFILL_HEADS, PREFILL_LENS
+
+    f = np.load(Path(__file__).resolve().parent / "golden" / "prefill_small.npz", allow_pickle=False)
+    c = oi.make_prefill_case(PREFILL_LENS, *PREFILL_HEADS, 128, seed=3)
+    assert c.fingerprint() == str(f["sha256"])
+    announce("prefill vs golden fixture")
+    out = _run(c, gpu, *PREFILL_HEADS)
+    ref = torch.from_numpy(f["closed_form_bf16"]).view(torch.bfloat16)
+    assert_close_attn(out, ref, "golden")
