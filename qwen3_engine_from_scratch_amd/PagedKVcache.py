@@ -21,7 +21,7 @@ import torch
 from . import _lib
 from .kernels.paged_attention import update_kv_batch_hip
 
-__all__ = ["KVCachePool", "PagedKVCache", "write_prefill_batch"]
+__all__ = ["KVCachePool", "PagedKVCache", "prefill_slot_mapping", "write_prefill_batch"]
 
 
 class KVCachePool:
