@@ -11,20 +11,23 @@
 //    sequence).  The head group holds HG query heads that share one KV head
 //    (HG = the largest of 4, 2, 1 dividing G), so a K/V tile staged in LDS
 //    serves every head of the group; each wave owns 32 query rows of one
-//    head.  Query tiles are dispatched heaviest-first (the causal row tile
-//    with the most keys first) to shorten the ragged tail.  Two workgroups
-//    share a CU (two waves per SIMD), so one wave's softmax overlaps the
-//    other's matrix-core work.
-//  * K/V tiles of 64 keys are double-buffered in LDS: the next tile's global
-//    loads are issued before the current tile's math and land in the other
-//    buffer after it, with a single barrier per tile.
+//    head.  Two workgroups share a CU (two waves per SIMD), so one wave's
+//    softmax overlaps the other's matrix-core work.
+//  * K/V tiles of 64 keys go from HBM straight into LDS with buffer loads
+//    that write LDS (no staging registers), double-buffered: the next tile's
+//    loads are issued before the current tile's math, with one barrier per
+//    tile.  The buffer descriptor covers only the sequence's rows, so rows
+//    past its end read as zero without a branch.
+//  * LDS tile layout: 64 key rows of 256 B, the 16-byte chunk c of row r at
+//    slot c ^ swz(r).  K uses swz = r % 16 (the QK operand reads one chunk
+//    of 16 consecutive rows per LDS cycle); V uses swz = 4 (r % 4) (the PV
+//    operand reads 64 B of 4 consecutive rows).  Both are conflict-free.
 //  * Scores are computed transposed, S^T(32 keys x 32 queries) = K Q^T with
 //    mfma_f32_32x32x16_bf16: each lane owns one query column and 16 of its
 //    keys, so the row max needs one cross-lane step, and the S^T register
-//    layout is directly the B operand (P^T) of O^T = V^T P^T.
-//  * V is staged into LDS transposed (V^T, one row per dim), once per
-//    workgroup, with the keys of each 16-key chunk stored in the order the
-//    P^T operand holds them, so each PV A operand is one 16-byte LDS read.
+//    layout is directly the B operand (P^T) of O^T = V^T P^T.  The V^T A
+//    operand comes from the row-major V tile with ds_read_b64_tr_b16, two
+//    transposing 8-byte reads per MFMA.
 //  * Softmax in the exp2 domain with the scale folded into one FMA; the
 //    running max is only raised (and the accumulator rescaled) when a new
 //    score exceeds it by more than 2^8, which keeps every P <= 256 and makes
@@ -34,13 +37,19 @@
 namespace {
 
 constexpr int kD = 128;
-constexpr int kBN = 64;              // keys per staged K/V tile
-constexpr int kKStride = kD + 8;     // K tile row (elements), padded
-constexpr int kVtStride = kBN + 8;   // V^T tile row (elements), padded
+constexpr int kBN = 64;                   // keys per staged K/V tile
+constexpr int kRowBytes = kD * 2;         // one staged key row (256 B)
+constexpr int kTileElems = kBN * kD;      // one staged K or V tile (16 KiB)
 constexpr int kWaves = 4;
-constexpr float kRescaleSlack = 8.f; // log2 headroom before the max is raised
-constexpr int kMaxSeqs = 256;         // persistent path: sequences ranked in LDS
-constexpr int kScanMax = 1024;        // persistent path: query-tile ranks in LDS
+constexpr int kDmaPerWave = kBN * kRowBytes / (kWaves * 64 * 16);  // 16-byte lanes
+constexpr float kRescaleSlack = 8.f;      // log2 headroom before the max is raised
+constexpr int kMaxSeqs = 256;             // persistent path: sequences ranked in LDS
+constexpr int kScanMax = 1024;            // persistent path: query-tile ranks in LDS
+static_assert(kDmaPerWave == 4, "tile / workgroup shape");
+
+typedef __attribute__((address_space(3))) void lds_void_t;
+typedef short i16x4 __attribute__((__vector_size__(4 * sizeof(short))));
+typedef __attribute__((address_space(3))) i16x4 lds_i16x4_t;
 
 struct PrefillArgs {
   const uint16_t* q;
@@ -57,73 +66,103 @@ struct PrefillArgs {
   int Hq, G, HG;
   int groups;    // query-head groups (Hq / HG)
   int rows;      // query rows per head per workgroup (32 * kWaves / HG)
-  int n_mtiles;  // grid.z
+  int n_mtiles;  // query tiles of the longest sequence
   float scale_log2;
   int causal;
 };
 
-// Position of key `key` (0..63) of a tile inside its V^T row: within each
-// 16-key chunk the P^T operand of lane half hl holds keys
-// {8a + 4hl + e : a, e}, stored contiguously at 8hl + 4a + e.
-__device__ __forceinline__ int vt_pos(int key) {
-  const int kc = key >> 4, a = (key >> 3) & 1, hl = (key >> 2) & 1, e = key & 3;
-  return 16 * kc + 8 * hl + 4 * a + e;
-}
-
-struct Staged {
-  q3::u32x4 k[4];  // K rows of this thread (16 bytes each)
-  q3::u32x4 v[4];  // V of keys 4*kg + i, dims 8*dg .. +7
+// The staged tiles of one workgroup: two K and two V buffers.
+struct TileBufs {
+  uint16_t* k0;
+  uint16_t* v0;
+  uint16_t* k1;
+  uint16_t* v1;
 };
 
-__device__ __forceinline__ void stage_load(Staged& st, const PrefillArgs& a, int64_t start,
-                                           int len, int kvh, int n0, int tid) {
-  const q3::u32x4 z = {0u, 0u, 0u, 0u};
+// Per-lane byte offsets that do not change from tile to tile.
+struct LaneOffsets {
+  uint32_t kdma[kDmaPerWave];  // source offset of this lane's K chunk, load j
+  uint32_t vdma[kDmaPerWave];  // same for V
+  uint32_t kread[8];           // LDS offset of the QK operand, d step t (key block 0)
+  uint32_t vread[4];           // LDS offset of the PV operand, d block db (key chunk 0)
+};
+
+__device__ __forceinline__ LaneOffsets lane_offsets(int lane, int wave, int64_t k_row_bytes,
+                                                    int64_t v_row_bytes) {
+  LaneOffsets o;
+  // Load j of wave w fills LDS block n = 4w + j (rows 4n .. 4n+3); lane i
+  // writes slot i % 16 of row 4n + i / 16, i.e. source chunk slot ^ swz(row).
 #pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    const int idx = tid + i * kWaves * 64;
-    const int r = idx >> 4;
-    const int c8 = (idx & 15) * 8;
-    st.k[i] = z;
-    if (n0 + r < len)
-      st.k[i] = q3::ld16(a.k + (start + n0 + r) * a.k_st + static_cast<int64_t>(kvh) * a.k_sh + c8);
+  for (int j = 0; j < kDmaPerWave; ++j) {
+    const int row = 4 * (kDmaPerWave * wave + j) + (lane >> 4);
+    const int slot = lane & 15;
+    o.kdma[j] = static_cast<uint32_t>(row * k_row_bytes) + ((slot ^ (row & 15)) << 4);
+    o.vdma[j] = static_cast<uint32_t>(row * v_row_bytes) + ((slot ^ (4 * (row & 3))) << 4);
   }
-  const int dg = tid >> 4, kg = tid & 15;
+  // QK A operand (mfma 32x32x16): lane reads key row lane % 32, chunk 2t + lane / 32.
+  const int r = lane & 31, h = lane >> 5;
 #pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    const int key = 4 * kg + i;
-    st.v[i] = z;
-    if (n0 + key < len)
-      st.v[i] = q3::ld16(a.v + (start + n0 + key) * a.v_st + static_cast<int64_t>(kvh) * a.v_sh +
-                         8 * dg);
+  for (int t = 0; t < 8; ++t) o.kread[t] = r * kRowBytes + ((((2 * t) | h) ^ (r & 15)) << 4);
+  // PV A operand (V^T) through ds_read_b64_tr_b16: in 16-lane group g, lane
+  // m supplies row 4 (g / 2) + m / 4 (+ 8 for the second read, + 16 per key
+  // chunk) and dims 32 db + 16 (g % 2) + 4 (m % 4) .. +3.
+  const int g = lane >> 4, m = lane & 15;
+  const int vrow = 4 * (g >> 1) + (m >> 2);
+#pragma unroll
+  for (int db = 0; db < 4; ++db) {
+    const int slot = 4 * (db ^ (m >> 2)) + 2 * (g & 1) + ((m & 3) >> 1);
+    o.vread[db] = vrow * kRowBytes + slot * 16 + 8 * (m & 1);
+  }
+  return o;
+}
+
+// Issues this wave's share of the loads of key tile n0 into (sk, sv).
+__device__ __forceinline__ void tile_dma(const PrefillArgs& a, const LaneOffsets& off,
+                                         int64_t start, int len, int kvh, int n0, uint16_t* sk,
+                                         uint16_t* sv, int wave) {
+  const int rows = min(kBN, len - n0);
+  const uint16_t* kb = a.k + (start + n0) * a.k_st + static_cast<int64_t>(kvh) * a.k_sh;
+  const uint16_t* vb = a.v + (start + n0) * a.v_st + static_cast<int64_t>(kvh) * a.v_sh;
+  // Rows past `rows` are outside the descriptor and read as zero.
+  const int k_bytes = static_cast<int>((rows - 1) * a.k_st * 2) + kRowBytes;
+  const int v_bytes = static_cast<int>((rows - 1) * a.v_st * 2) + kRowBytes;
+  const __amdgpu_buffer_rsrc_t kr =
+      __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t*>(kb), 0, k_bytes, 0x00020000);
+  const __amdgpu_buffer_rsrc_t vr =
+      __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t*>(vb), 0, v_bytes, 0x00020000);
+#pragma unroll
+  for (int j = 0; j < kDmaPerWave; ++j) {
+    const int blk = (kDmaPerWave * wave + j) * 512;  // elements: 1 KiB per load
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(kr, (lds_void_t*)(sk + blk), 16, off.kdma[j], 0, 0, 0);
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(vr, (lds_void_t*)(sv + blk), 16, off.vdma[j], 0, 0, 0);
   }
 }
 
-__device__ __forceinline__ void stage_store(const Staged& st, uint16_t* s_k, uint16_t* s_vt,
-                                            int tid) {
-#pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    const int idx = tid + i * kWaves * 64;
-    const int r = idx >> 4;
-    const int c8 = (idx & 15) * 8;
-    *reinterpret_cast<q3::u32x4*>(&s_k[r * kKStride + c8]) = st.k[i];
-  }
-  // Transpose the 4 keys x 8 dims block: dim 8*dg + j gets keys 4*kg .. +3.
-  const int dg = tid >> 4, kg = tid & 15;
-  const int pos = vt_pos(4 * kg);
-#pragma unroll
-  for (int j = 0; j < 8; ++j) {
-    const int w = j >> 1, h = j & 1;
-    q3::u32x2 col = {q3::pick_halves(st.v[0][w], st.v[1][w], h),
-                     q3::pick_halves(st.v[2][w], st.v[3][w], h)};
-    *reinterpret_cast<q3::u32x2*>(&s_vt[(8 * dg + j) * kVtStride + pos]) = col;
-  }
+__device__ __forceinline__ q3::bf16x8 lds_ld16(const uint16_t* base, uint32_t byte_off) {
+  return q3::as_bf16x8(
+      *reinterpret_cast<const q3::u32x4*>(reinterpret_cast<const char*>(base) + byte_off));
+}
+
+// V^T operand: two transposing 8-byte reads (keys +0..3 and +8..11 of the
+// lane half's key set).
+__device__ __forceinline__ q3::bf16x8 lds_vt(const uint16_t* base, uint32_t byte_off) {
+  const char* p = reinterpret_cast<const char*>(base) + byte_off;
+  const i16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4_t*)(p));
+  const i16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4_t*)(p + 8 * kRowBytes));
+  typedef short i16x8 __attribute__((__vector_size__(8 * sizeof(short))));
+  const i16x8 both = __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
+  return __builtin_bit_cast(q3::bf16x8, both);
+}
+
+__device__ __forceinline__ void wait_loads() {
+  // vmcnt(0) with expcnt / lgkmcnt left at their maxima.
+  __builtin_amdgcn_s_waitcnt(0x0f70);
 }
 
 // One work item: query tile mt of sequence seq for head group hg.  Every
-// thread of the workgroup calls it; s_k / s_vt are the two LDS tile buffers.
-__device__ __forceinline__ void prefill_item(const PrefillArgs& a, int seq, int hg, int mt,
-                                             uint16_t (*s_k)[kBN * kKStride],
-                                             uint16_t (*s_vt)[kD * kVtStride]) {
+// thread of the workgroup calls it.
+__device__ __forceinline__ void prefill_item(const PrefillArgs& a, const LaneOffsets& off,
+                                             int seq, int hg, int mt, const TileBufs& tb) {
   const int64_t start = a.cu[seq];
   const int64_t end = a.cu[seq + 1];
   if (start < 0 || end > a.total || end <= start) return;
@@ -145,8 +184,7 @@ __device__ __forceinline__ void prefill_item(const PrefillArgs& a, int seq, int 
   const int kend = a.causal ? min(len, m0 + a.rows) : len;
   const int n_tiles = (kend + kBN - 1) / kBN;
 
-  Staged stg;
-  stage_load(stg, a, start, len, kvh, 0, tid);
+  tile_dma(a, off, start, len, kvh, 0, tb.k0, tb.v0, wave);
 
   // Q^T as the B operand: lane (query l32, k-group hl), chunk c: dims
   // c*16 + 8*hl .. +7.
@@ -160,9 +198,6 @@ __device__ __forceinline__ void prefill_item(const PrefillArgs& a, int seq, int 
     for (int c = 0; c < 8; ++c) qv[c] = q3::as_bf16x8(ok ? q3::ld16(qp + c * 16) : z);
   }
 
-  stage_store(stg, s_k[0], s_vt[0], tid);
-  __syncthreads();
-
   float m_run = q3::kNegInf;  // running max (log2 domain) of this query
   float l_run = 0.f;          // this lane's share of the denominator
   q3::f32x16 acc[4];          // acc[db][r] = O[qrow][32*db + 8*(r/4) + 4*hl + r%4]
@@ -175,29 +210,25 @@ __device__ __forceinline__ void prefill_item(const PrefillArgs& a, int seq, int 
   const int wave_last_q = min(q0 + 31, len - 1);
   const float c = a.scale_log2;
 
-  for (int it = 0; it < n_tiles; ++it) {
+  wait_loads();
+  __syncthreads();
+
+  auto tile = [&](int it, const uint16_t* kt, const uint16_t* vt, uint16_t* nk, uint16_t* nv) {
     const int n0 = it * kBN;
-    const int buf = it & 1;
-    const bool more = it + 1 < n_tiles;
-    if (more) stage_load(stg, a, start, len, kvh, n0 + kBN, tid);
+    if (it + 1 < n_tiles) tile_dma(a, off, start, len, kvh, n0 + kBN, nk, nv, wave);
 
     // Causal: the tile is entirely above this wave's last query row.
     const bool wave_skip = !wave_active || (a.causal && n0 > wave_last_q);
     if (!wave_skip) {
-      const uint16_t* kt = s_k[buf];
-      const uint16_t* vt = s_vt[buf];
       // ---- S^T = K Q^T for two 32-key blocks ----
       q3::f32x16 s[2];
 #pragma unroll
       for (int kb = 0; kb < 2; ++kb) {
 #pragma unroll
         for (int r = 0; r < 16; ++r) s[kb][r] = 0.f;
-        const uint16_t* kp = kt + (kb * 32 + l32) * kKStride + 8 * hl;
 #pragma unroll
-        for (int cc = 0; cc < 8; ++cc) {
-          const q3::bf16x8 kf = q3::as_bf16x8(*reinterpret_cast<const q3::u32x4*>(kp + cc * 16));
-          s[kb] = q3::mfma32x32x16(kf, qv[cc], s[kb]);
-        }
+        for (int t = 0; t < 8; ++t)
+          s[kb] = q3::mfma32x32x16(lds_ld16(kt, off.kread[t] + kb * 32 * kRowBytes), qv[t], s[kb]);
       }
       // ---- mask (diagonal / tail tiles only) and block max ----
       const bool need_mask = (n0 + kBN > len) || (a.causal && n0 + kBN - 1 > q0);
@@ -253,15 +284,18 @@ __device__ __forceinline__ void prefill_item(const PrefillArgs& a, int seq, int 
         for (int kc = 0; kc < 2; ++kc) {
           const int KC = 2 * kb + kc;
 #pragma unroll
-          for (int db = 0; db < 4; ++db) {
-            const q3::bf16x8 vf = q3::as_bf16x8(*reinterpret_cast<const q3::u32x4*>(
-                vt + (32 * db + l32) * kVtStride + 16 * KC + 8 * hl));
-            acc[db] = q3::mfma32x32x16(vf, p[kb][kc], acc[db]);
-          }
+          for (int db = 0; db < 4; ++db)
+            acc[db] = q3::mfma32x32x16(lds_vt(vt, off.vread[db] + KC * 16 * kRowBytes),
+                                       p[kb][kc], acc[db]);
         }
     }
-    if (more) stage_store(stg, s_k[buf ^ 1], s_vt[buf ^ 1], tid);
+    wait_loads();
     __syncthreads();
+  };
+
+  for (int it = 0; it < n_tiles; it += 2) {
+    tile(it, tb.k0, tb.v0, tb.k1, tb.v1);
+    if (it + 1 < n_tiles) tile(it + 1, tb.k1, tb.v1, tb.k0, tb.v0);
   }
 
   if (!wave_active || qrow >= len) return;
@@ -279,6 +313,15 @@ __device__ __forceinline__ void prefill_item(const PrefillArgs& a, int seq, int 
     }
 }
 
+// The four staged tile buffers, as separate LDS arrays so loads into one
+// buffer are known not to alias reads of the other.
+#define Q3_PREFILL_TILE_BUFFERS                                        \
+  __shared__ __attribute__((aligned(1024))) uint16_t s_k0[kTileElems]; \
+  __shared__ __attribute__((aligned(1024))) uint16_t s_v0[kTileElems]; \
+  __shared__ __attribute__((aligned(1024))) uint16_t s_k1[kTileElems]; \
+  __shared__ __attribute__((aligned(1024))) uint16_t s_v1[kTileElems]; \
+  const TileBufs tb{s_k0, s_v0, s_k1, s_v1};                           \
+  const LaneOffsets off = lane_offsets(threadIdx.x & 63, threadIdx.x >> 6, a.k_st * 2, a.v_st * 2)
 
 // Flat grid (fallback for many sequences / very long ones): one workgroup
 // per virtual item, head group fastest so consecutive workgroups go to
@@ -286,14 +329,13 @@ __device__ __forceinline__ void prefill_item(const PrefillArgs& a, int seq, int 
 // heaviest first.  Items past a sequence's end exit at once.
 __global__ __launch_bounds__(kWaves * 64) __attribute__((amdgpu_waves_per_eu(2, 2)))
 void varlen_prefill_flat_kernel(PrefillArgs a) {
-  __shared__ uint16_t s_k[2][kBN * kKStride];
-  __shared__ uint16_t s_vt[2][kD * kVtStride];
+  Q3_PREFILL_TILE_BUFFERS;
   const int64_t id = blockIdx.x;
   const int hg = static_cast<int>(id % a.groups);
   const int seq = static_cast<int>((id / a.groups) % a.num_seqs);
   const int mt =
       a.n_mtiles - 1 - static_cast<int>(id / (static_cast<int64_t>(a.groups) * a.num_seqs));
-  prefill_item(a, seq, hg, mt, s_k, s_vt);
+  prefill_item(a, off, seq, hg, mt, tb);
 }
 
 // Exclusive prefix sum over n <= kScanMax ints held in LDS (in place); returns
@@ -345,8 +387,7 @@ __device__ __forceinline__ int block_exclusive_scan(int* v, int n, int* s_wsum) 
 __global__ __launch_bounds__(kWaves * 64)
 __attribute__((amdgpu_waves_per_eu(Q3_PREFILL_PERSISTENT_WAVES_PER_EU, Q3_PREFILL_PERSISTENT_WAVES_PER_EU)))
 void varlen_prefill_persistent_kernel(PrefillArgs a) {
-  __shared__ uint16_t s_k[2][kBN * kKStride];
-  __shared__ uint16_t s_vt[2][kD * kVtStride];
+  Q3_PREFILL_TILE_BUFFERS;
   __shared__ int s_len[kMaxSeqs];
   __shared__ int s_sorted[kMaxSeqs];
   __shared__ int s_first[kScanMax];  // items before m-tile rank r (r = n_mtiles-1-mt)
@@ -401,7 +442,7 @@ void varlen_prefill_persistent_kernel(PrefillArgs a) {
     const int seq = s_sorted[j / a.groups];
     const int hg = j % a.groups;
     __syncthreads();  // the previous item's LDS tiles are no longer read
-    prefill_item(a, seq, hg, nm - 1 - lo, s_k, s_vt);
+    prefill_item(a, off, seq, hg, nm - 1 - lo, tb);
   }
 }
 
