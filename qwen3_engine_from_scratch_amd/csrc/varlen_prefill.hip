@@ -154,6 +154,19 @@ __device__ __forceinline__ q3::bf16x8 lds_vt(const uint16_t* base, uint32_t byte
   return __builtin_bit_cast(q3::bf16x8, both);
 }
 
+// LDS operand distance of the MFMA loops (steps read ahead).
+constexpr int kAhead = 4;
+
+// Byte offset of the K operand of QK step u (key block u % 2, d step u / 2).
+__device__ __forceinline__ uint32_t qk_operand(const LaneOffsets& off, int u) {
+  return off.kread[u >> 1] + (u & 1) * 32 * kRowBytes;
+}
+
+// Byte offset of the V^T operand of PV step u (key chunk u / 4, d block u % 4).
+__device__ __forceinline__ uint32_t pv_operand(const LaneOffsets& off, int u) {
+  return off.vread[u & 3] + (u >> 2) * 16 * kRowBytes;
+}
+
 __device__ __forceinline__ void wait_loads() {
   // vmcnt(0) with expcnt / lgkmcnt left at their maxima.
   __builtin_amdgcn_s_waitcnt(0x0f70);
@@ -172,7 +185,7 @@ __device__ __forceinline__ void prefill_item(const PrefillArgs& a, const LaneOff
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
-  const int wave = tid >> 6;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // uniform: scalar branches
   const int l32 = lane & 31;
   const int hl = lane >> 5;
   const int wph = kWaves / a.HG;  // waves per head
@@ -221,14 +234,25 @@ __device__ __forceinline__ void prefill_item(const PrefillArgs& a, const LaneOff
     const bool wave_skip = !wave_active || (a.causal && n0 > wave_last_q);
     if (!wave_skip) {
       // ---- S^T = K Q^T for two 32-key blocks ----
+      // Step u covers key block u % 2, dims 16 (u / 2) .. +15; the two
+      // blocks' chains alternate and K operands are read 4 steps ahead (the
+      // scheduling fences keep that distance).
       q3::f32x16 s[2];
 #pragma unroll
-      for (int kb = 0; kb < 2; ++kb) {
+      for (int kb = 0; kb < 2; ++kb)
 #pragma unroll
         for (int r = 0; r < 16; ++r) s[kb][r] = 0.f;
+      {
+        q3::bf16x8 kf[kAhead];
 #pragma unroll
-        for (int t = 0; t < 8; ++t)
-          s[kb] = q3::mfma32x32x16(lds_ld16(kt, off.kread[t] + kb * 32 * kRowBytes), qv[t], s[kb]);
+        for (int u = 0; u < kAhead; ++u) kf[u] = lds_ld16(kt, qk_operand(off, u));
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int u = 0; u < 16; ++u) {
+          s[u & 1] = q3::mfma32x32x16(kf[u % kAhead], qv[u >> 1], s[u & 1]);
+          if (u + kAhead < 16) kf[u % kAhead] = lds_ld16(kt, qk_operand(off, u + kAhead));
+          __builtin_amdgcn_sched_barrier(0);
+        }
       }
       // ---- mask (diagonal / tail tiles only) and block max ----
       const bool need_mask = (n0 + kBN > len) || (a.causal && n0 + kBN - 1 > q0);
@@ -258,9 +282,15 @@ __device__ __forceinline__ void prefill_item(const PrefillArgs& a, const LaneOff
 #pragma unroll
         for (int db = 0; db < 4; ++db) acc[db] *= alpha;
       }
+      // V^T operands of the first PV steps are read before the exponentials,
+      // which hide their latency.
+      q3::bf16x8 vf[kAhead];
+#pragma unroll
+      for (int u = 0; u < kAhead; ++u) vf[u] = lds_vt(vt, pv_operand(off, u));
+      __builtin_amdgcn_sched_barrier(0);
       const float m_use = m_run == q3::kNegInf ? 0.f : m_run;
-      // ---- P = exp2(s * c - m), P^T as B operands (registers 8*kc .. +7) ----
-      q3::bf16x8 p[2][2];
+      // ---- P = exp2(s * c - m), P^T as B operands (chunk KC = 2 kb + kc) ----
+      q3::bf16x8 p[4];
       float psum = 0.f;
 #pragma unroll
       for (int kb = 0; kb < 2; ++kb)
@@ -274,20 +304,17 @@ __device__ __forceinline__ void prefill_item(const PrefillArgs& a, const LaneOff
           }
           q3::u32x4 pk = {q3::pack_bf16x2(e[0], e[1]), q3::pack_bf16x2(e[2], e[3]),
                           q3::pack_bf16x2(e[4], e[5]), q3::pack_bf16x2(e[6], e[7])};
-          p[kb][kc] = q3::as_bf16x8(pk);
+          p[2 * kb + kc] = q3::as_bf16x8(pk);
         }
       l_run += psum;
-      // ---- O^T += V^T P^T: chunk KC = 2*kb + kc of 16 keys ----
+      __builtin_amdgcn_sched_barrier(0);
+      // ---- O^T += V^T P^T: step u covers key chunk u / 4, dims 32 (u % 4) .. +31 ----
 #pragma unroll
-      for (int kb = 0; kb < 2; ++kb)
-#pragma unroll
-        for (int kc = 0; kc < 2; ++kc) {
-          const int KC = 2 * kb + kc;
-#pragma unroll
-          for (int db = 0; db < 4; ++db)
-            acc[db] = q3::mfma32x32x16(lds_vt(vt, off.vread[db] + KC * 16 * kRowBytes),
-                                       p[kb][kc], acc[db]);
-        }
+      for (int u = 0; u < 16; ++u) {
+        acc[u & 3] = q3::mfma32x32x16(vf[u % kAhead], p[u >> 2], acc[u & 3]);
+        if (u + kAhead < 16) vf[u % kAhead] = lds_vt(vt, pv_operand(off, u + kAhead));
+        __builtin_amdgcn_sched_barrier(0);
+      }
     }
     wait_loads();
     __syncthreads();
