@@ -167,6 +167,52 @@ __device__ __forceinline__ uint32_t pv_operand(const LaneOffsets& off, int u) {
   return off.vread[u & 3] + (u >> 2) * 16 * kRowBytes;
 }
 
+// Maximum of the 32 scores s[0..1][0..15] of one lane: four interleaved
+// v_max3 chains of eight scores and a final combine (depth 6).  Written as
+// one asm block because fmaxf would first canonicalize every MFMA result;
+// a NaN score makes P, and so the output, NaN either way.
+__device__ __forceinline__ float max3_scores(const q3::f32x16 (&s)[2]) {
+  const q3::f32x16& a = s[0];
+  const q3::f32x16& b = s[1];
+  float m, t1, t2, t3;
+  asm volatile(
+      "v_max3_f32 %0, %4, %5, %6\n\t"
+      "v_max3_f32 %1, %12, %13, %14\n\t"
+      "v_max3_f32 %2, %20, %21, %22\n\t"
+      "v_max3_f32 %3, %28, %29, %30\n\t"
+      "v_max3_f32 %0, %0, %7, %8\n\t"
+      "v_max3_f32 %1, %1, %15, %16\n\t"
+      "v_max3_f32 %2, %2, %23, %24\n\t"
+      "v_max3_f32 %3, %3, %31, %32\n\t"
+      "v_max3_f32 %0, %0, %9, %10\n\t"
+      "v_max3_f32 %1, %1, %17, %18\n\t"
+      "v_max3_f32 %2, %2, %25, %26\n\t"
+      "v_max3_f32 %3, %3, %33, %34\n\t"
+      "v_max3_f32 %0, %0, %11, %19\n\t"
+      "v_max3_f32 %2, %2, %27, %35\n\t"
+      "v_max3_f32 %0, %0, %1, %2\n\t"
+      "v_max_f32 %0, %0, %3"
+      : "=&v"(m), "=&v"(t1), "=&v"(t2), "=&v"(t3)
+      : "v"(a[0]), "v"(a[1]), "v"(a[2]), "v"(a[3]), "v"(a[4]), "v"(a[5]), "v"(a[6]), "v"(a[7]),
+        "v"(a[8]), "v"(a[9]), "v"(a[10]), "v"(a[11]), "v"(a[12]), "v"(a[13]), "v"(a[14]),
+        "v"(a[15]), "v"(b[0]), "v"(b[1]), "v"(b[2]), "v"(b[3]), "v"(b[4]), "v"(b[5]), "v"(b[6]),
+        "v"(b[7]), "v"(b[8]), "v"(b[9]), "v"(b[10]), "v"(b[11]), "v"(b[12]), "v"(b[13]),
+        "v"(b[14]), "v"(b[15]));
+  return m;
+}
+
+// x combined with the value lane l ^ 32 holds: v_permlane32_swap of x with
+// itself leaves the lower-half value in r[0] and the upper-half value in
+// r[1] on every lane.
+__device__ __forceinline__ float cross_half_max(float x) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+__device__ __forceinline__ float cross_half_sum(float x) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+
 __device__ __forceinline__ void wait_loads() {
   // vmcnt(0) with expcnt / lgkmcnt left at their maxima.
   __builtin_amdgcn_s_waitcnt(0x0f70);
@@ -266,12 +312,14 @@ __device__ __forceinline__ void prefill_item(const PrefillArgs& a, const LaneOff
             s[kb][r] = valid ? s[kb][r] : q3::kNegInf;
           }
       }
-      float bm = q3::kNegInf;
-#pragma unroll
-      for (int kb = 0; kb < 2; ++kb)
-#pragma unroll
-        for (int r = 0; r < 16; r += 2) bm = fmaxf(bm, fmaxf(s[kb][r], s[kb][r + 1]));
-      bm = fmaxf(bm, q3::shfl_xor(bm, 32));
+      // Row max as a v_max3 chain over the lane's 32 scores.  Written as asm
+      // because fmaxf would first canonicalize every MFMA result (one more
+      // VALU op per score); a NaN score makes P, and so the output, NaN
+      // either way.  The scores were written by the QK MFMAs just above:
+      // 24 wait states cover the MFMA-to-VALU dependency.
+      asm volatile("s_nop 7\n\ts_nop 7\n\ts_nop 7");
+      float bm = max3_scores(s);
+      bm = cross_half_max(bm);
       const float m_cand = bm * c;
       const bool raise = m_cand > m_run + kRescaleSlack;
       if (__any(raise)) {
@@ -291,7 +339,7 @@ __device__ __forceinline__ void prefill_item(const PrefillArgs& a, const LaneOff
       const float m_use = m_run == q3::kNegInf ? 0.f : m_run;
       // ---- P = exp2(s * c - m), P^T as B operands (chunk KC = 2 kb + kc) ----
       q3::bf16x8 p[4];
-      float psum = 0.f;
+      float psum[4] = {0.f, 0.f, 0.f, 0.f};  // four independent sum chains
 #pragma unroll
       for (int kb = 0; kb < 2; ++kb)
 #pragma unroll
@@ -300,13 +348,13 @@ __device__ __forceinline__ void prefill_item(const PrefillArgs& a, const LaneOff
 #pragma unroll
           for (int i = 0; i < 8; ++i) {
             e[i] = q3::fast_exp2(__builtin_fmaf(s[kb][8 * kc + i], c, -m_use));
-            psum += e[i];
+            psum[i & 3] += e[i];
           }
           q3::u32x4 pk = {q3::pack_bf16x2(e[0], e[1]), q3::pack_bf16x2(e[2], e[3]),
                           q3::pack_bf16x2(e[4], e[5]), q3::pack_bf16x2(e[6], e[7])};
           p[2 * kb + kc] = q3::as_bf16x8(pk);
         }
-      l_run += psum;
+      l_run += (psum[0] + psum[1]) + (psum[2] + psum[3]);
       __builtin_amdgcn_sched_barrier(0);
       // ---- O^T += V^T P^T: step u covers key chunk u / 4, dims 32 (u % 4) .. +31 ----
 #pragma unroll
@@ -325,8 +373,8 @@ __device__ __forceinline__ void prefill_item(const PrefillArgs& a, const LaneOff
     if (it + 1 < n_tiles) tile(it + 1, tb.k1, tb.v1, tb.k0, tb.v0);
   }
 
+  l_run = cross_half_sum(l_run);
   if (!wave_active || qrow >= len) return;
-  l_run += q3::shfl_xor(l_run, 32);
   const float inv = l_run > 0.f ? 1.f / l_run : 0.f;
   uint16_t* op = a.o + (start + qrow) * a.o_st + static_cast<int64_t>(head) * a.o_sh;
 #pragma unroll
