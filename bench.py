@@ -180,6 +180,32 @@ def bench_prefill(args, dev):
     from qwen3_engine_from_scratch_amd import _lib
     from qwen3_engine_from_scratch_amd.kernels.flash_attention_varlen import flash_attention_prefill
 
+    if args.prefill_workload == "steady":
+        # 8 x 4096 tokens, non-causal: every query tile sweeps every key tile,
+        # no masking and no ragged tail (the kernel's steady-state rate).
+        lens = [4096] * 8
+        g = torch.Generator(device=dev).manual_seed(0)
+        q = torch.randn(sum(lens), 16, 128, device=dev, generator=g).to(torch.bfloat16)
+        k = torch.randn(sum(lens), 8, 128, device=dev, generator=g).to(torch.bfloat16)
+        v = torch.randn(sum(lens), 8, 128, device=dev, generator=g).to(torch.bfloat16)
+        cu = torch.tensor([0] + [4096 * (i + 1) for i in range(8)], dtype=torch.int32, device=dev)
+        out = torch.empty_like(q)
+
+        def sstep():
+            flash_attention_prefill(q, k, v, cu, 128 ** -0.5, 16, 8, 128, max_seqlen=4096,
+                                    causal=False, out=out)
+
+        _, s_evt = time_steps(sstep, args.steps, args.warmup)
+        flops = 4 * 128 * 16 * sum(L * L for L in lens)
+        tflops = flops / (s_evt * 1e-3) / 1e12
+        log(f"prefill (steady, 8x4096 non-causal): {s_evt * 1e3:.1f} us/call, {tflops:.1f} TFLOP/s")
+        return {"workload": "varlen non-causal prefill, 8 x 4096 tokens, 16/8 heads, head_dim 128, bf16",
+                "value": round(tflops, 2), "unit": "TFLOP/s", "ms_per_step": round(s_evt, 5),
+                "flops": flops,
+                "roofline": {"bound": "mfma", "achieved": round(tflops, 2),
+                             "peak": MFMA_BF16_PEAK_TFLOPS, "unit": "TFLOP/s",
+                             "frac": round(tflops / MFMA_BF16_PEAK_TFLOPS, 4), "traffic": None}}
+
     c = oi.config2_prefill()
     q, k, v = c.q.to(dev), c.k.to(dev), c.v.to(dev)
     cu = c.cu_seqlens.to(dev)
@@ -229,6 +255,9 @@ def main(argv=None):
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--only", choices=["decode", "prefill"], default=None)
     ap.add_argument("--workload", choices=["config3", "config4"], default="config3")
+    ap.add_argument("--prefill-workload", choices=["config2", "steady"], default="config2",
+                    help="prefill line: the Qwen3-0.6B ragged causal batch, or 8 x 4096 tokens "
+                         "non-causal (steady-state rate; profiling only, with --only prefill)")
     ap.add_argument("--cpu-sample", type=int, default=64, help="sequences in the CPU baseline sample")
     ap.add_argument("--no-long-context", action="store_true",
                     help="skip the secondary long-context (B=8, up to 128k tokens) decode line")
@@ -236,6 +265,8 @@ def main(argv=None):
                     help="also run a plain 1 GiB device copy (the known-size reference for "
                          "rocprofv3 FETCH_SIZE / WRITE_SIZE counters)")
     args = ap.parse_args(argv)
+    if args.prefill_workload != "config2" and args.only != "prefill":
+        ap.error("--prefill-workload steady is a profiling line: use it with --only prefill")
     if args.gpus != 1:
         print(f"bench.py measures one GPU only: this build has no multi-GPU path "
               f"(asked for --gpus {args.gpus}); run with --gpus 1", file=sys.stderr)
