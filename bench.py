@@ -91,19 +91,40 @@ def time_steps(fn, steps, warmup):
     return wall, evt
 
 
+def seeded_lengths(n: int, lo: int, hi: int, seed: int = 0) -> list:
+    """n lengths uniform in [lo, hi] from a seeded CPU generator."""
+    import torch
+
+    g = torch.Generator().manual_seed(seed)
+    return [int(x) for x in torch.randint(lo, hi + 1, (n,), generator=g)]
+
+
+# The workloads (seed 0): Qwen3-0.6B varlen prefill (8 lengths in [64, 2048]),
+# the Qwen3-8B decode headline (256 contexts in [1024, 8192]) and the
+# long-context decode (8 contexts in [32768, 131072]).
+WORKLOAD_LENGTHS = {
+    "config2": (8, 64, 2048),
+    "config3": (256, 1024, 8192),
+    "config4": (8, 32768, 131072),
+}
+
+
+def workload_lengths(name: str) -> list:
+    return seeded_lengths(*WORKLOAD_LENGTHS[name])
+
+
 def bench_decode(args, dev):
     import torch
 
-    from oracle import inputs as oi
     from qwen3_engine_from_scratch_amd.kernels.paged_attention import (
         paged_attention_decode_hip, paged_decode_workspace_bytes)
 
     if args.workload == "config4":
-        lens, wname = oi.config4_lengths(), ("long-context split-KV paged decode, Qwen3-8B shape: "
-                                             "B=8, L~U[32768,131072]")
+        lens, wname = workload_lengths("config4"), ("long-context split-KV paged decode, Qwen3-8B "
+                                                    "shape: B=8, L~U[32768,131072]")
     else:
-        lens, wname = oi.config3_lengths(), ("paged decode attention, Qwen3-8B shape: B=256, "
-                                             "L~U[1024,8192]")
+        lens, wname = workload_lengths("config3"), ("paged decode attention, Qwen3-8B shape: "
+                                                    "B=256, L~U[1024,8192]")
     hq, hkv = 32, 8
     log(f"decode inputs: B={len(lens)} sumL={sum(lens)}")
     t = decode_inputs(lens, hq, hkv, dev)
@@ -173,12 +194,96 @@ def profiled_traffic(name: str):
     return None
 
 
+def bench_pre_attention(args, dev):
+    """Fused QK-RMSNorm + RoPE + pool write, HBM-bound: the slot form over the
+    Qwen3-0.6B prefill batch (8,115 tokens, 16 / 8 heads) and the decode form
+    for one Qwen3-8B layer at B=256 (32 / 8 heads; a few MB, launch-bound)."""
+    import torch
+
+    from qwen3_engine_from_scratch_amd.kernels.pre_attention import (
+        qk_norm_rope_decode, qk_norm_rope_prefill, rope_tables)
+
+    cos, sin = rope_tables(128, 1e6, 4096, device=dev)
+    g = torch.Generator(device=dev).manual_seed(0)
+    res = {}
+
+    lens = workload_lengths("config2")
+    T = sum(lens)
+    hq, hkv = 16, 8
+    qkv = torch.randn(T, (hq + 2 * hkv) * 128, device=dev, generator=g).to(torch.bfloat16)
+    q = qkv[:, :hq * 128].view(T, hq, 128)
+    k = qkv[:, hq * 128:(hq + hkv) * 128].view(T, hkv, 128)
+    v = qkv[:, (hq + hkv) * 128:].view(T, hkv, 128)
+    w = torch.ones(128, dtype=torch.bfloat16, device=dev)
+    pos = torch.cat([torch.arange(L, device=dev) for L in lens])
+    nblk = (T + 15) // 16 + 8
+    slots = torch.randperm(nblk * 16, device=dev, generator=g)[:T]
+    kb = torch.zeros(nblk, 1, hkv, 16, 128, dtype=torch.bfloat16, device=dev)
+    vb = torch.zeros_like(kb)
+    qo = torch.empty(T, hq, 128, dtype=torch.bfloat16, device=dev)
+    ko = torch.empty(T, hkv, 128, dtype=torch.bfloat16, device=dev)
+
+    def pstep():
+        qk_norm_rope_prefill(q, k, v, w, w, 1e-6, cos, sin, pos, slots, kb, vb, 0, qo, ko)
+
+    _, p_evt = time_steps(pstep, args.steps, args.warmup)
+    # per token: q, k, v read, one cos and one sin row, position + slot;
+    # q_out, k_out, pool k and pool v written
+    pbytes = T * ((hq + 2 * hkv) * 256 + 2 * 128 * 4 + 16 + (hq + 3 * hkv) * 256)
+    gbs = pbytes / (p_evt * 1e-3) / 1e9
+    log(f"pre-attention (prefill, {T} tokens): {p_evt * 1e3:.1f} us/call, {gbs:.0f} GB/s")
+    res["prefill"] = {"workload": f"Qwen3-0.6B prefill batch, {T} tokens, 16/8 heads",
+                      "ms_per_step": round(p_evt, 5), "bytes": pbytes, "GB/s": round(gbs, 1),
+                      "frac_hbm_peak": round(gbs / HBM_PEAK_GBS, 4)}
+    del qkv, q, k, v, kb, vb, qo, ko
+
+    from qwen3_engine_from_scratch_amd.PagedKVcache import KVCachePool
+    B, hq, hkv = 256, 32, 8
+    pool = KVCachePool(B * 2 + 8, 1, 16, hkv, 128, device=dev, dtype=torch.bfloat16,
+                       max_seq_len=4096, max_requests=B)
+    lens_d = torch.randint(1, 4000, (B,), device=dev, generator=g, dtype=torch.int32)
+    pool.seq_lens[:B] = lens_d
+    pages = (lens_d.long() + 16) // 16
+    tab = torch.randint(0, B * 2 + 8, (B, pool.block_table_2d.shape[1]), device=dev,
+                        generator=g, dtype=torch.int32)
+    pool.block_table_2d[:B] = torch.where(
+        torch.arange(tab.shape[1], device=dev)[None, :] < pages[:, None], tab, -1)
+    qkv = torch.randn(B, (hq + 2 * hkv) * 128, device=dev, generator=g).to(torch.bfloat16)
+    q = qkv[:, :hq * 128].view(B, hq, 128)
+    k = qkv[:, hq * 128:(hq + hkv) * 128].view(B, hkv, 128)
+    v = qkv[:, (hq + hkv) * 128:].view(B, hkv, 128)
+    rows = torch.arange(B, dtype=torch.int32, device=dev)
+    qd = torch.empty(B, hq, 128, dtype=torch.bfloat16, device=dev)
+
+    # A decode layer step is a few MB: time it as the engine runs it, inside a
+    # captured graph (10 calls per replay), so host launch cost is not measured.
+    for _ in range(3):
+        qk_norm_rope_decode(q, k, v, w, w, 1e-6, cos, sin, pool, 0, rows, qd)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        for _ in range(10):
+            qk_norm_rope_decode(q, k, v, w, w, 1e-6, cos, sin, pool, 0, rows, qd)
+
+    def dstep():
+        graph.replay()
+
+    _, d_evt = time_steps(dstep, args.steps, args.warmup)
+    d_evt /= 10
+    dbytes = B * ((hq + 2 * hkv) * 256 + 2 * 128 * 4 + 16 + (hq + 2 * hkv) * 256)
+    log(f"pre-attention (decode, B={B}, 32/8 heads, graph replay): {d_evt * 1e3:.2f} us/call")
+    res["decode"] = {"workload": f"one Qwen3-8B layer, B={B} decode tokens, 32/8 heads",
+                     "ms_per_step": round(d_evt, 5), "bytes": dbytes,
+                     "GB/s": round(dbytes / (d_evt * 1e-3) / 1e9, 1)}
+    return res
+
+
 def bench_prefill(args, dev):
     import torch
 
-    from oracle import inputs as oi
     from qwen3_engine_from_scratch_amd import _lib
     from qwen3_engine_from_scratch_amd.kernels.flash_attention_varlen import flash_attention_prefill
+    from qwen3_engine_from_scratch_amd.kernels.pre_attention import qk_norm_rope_prefill, rope_tables
 
     if args.prefill_workload == "steady":
         # 8 x 4096 tokens, non-causal: every query tile sweeps every key tile,
@@ -206,37 +311,54 @@ def bench_prefill(args, dev):
                              "peak": MFMA_BF16_PEAK_TFLOPS, "unit": "TFLOP/s",
                              "frac": round(tflops / MFMA_BF16_PEAK_TFLOPS, 4), "traffic": None}}
 
-    c = oi.config2_prefill()
-    q, k, v = c.q.to(dev), c.k.to(dev), c.v.to(dev)
-    cu = c.cu_seqlens.to(dev)
+    # Qwen3-0.6B batch: N(0,1) projections, QK-RMSNorm (weights 1 + 0.1 N(0,1))
+    # and RoPE at positions 0..L-1 applied by the fused pre-attention kernel.
+    lens = workload_lengths("config2")
+    T = sum(lens)
+    g = torch.Generator(device=dev).manual_seed(0)
+    qkv = torch.randn(T, 32 * 128, device=dev, generator=g).to(torch.bfloat16)
+    qw = (1 + 0.1 * torch.randn(128, device=dev, generator=g)).to(torch.bfloat16)
+    kw = (1 + 0.1 * torch.randn(128, device=dev, generator=g)).to(torch.bfloat16)
+    cos, sin = rope_tables(128, 1e6, 4096, device=dev)
+    pos = torch.cat([torch.arange(L, device=dev) for L in lens])
+    none_pool = torch.zeros(1, 1, 8, 16, 128, dtype=torch.bfloat16, device=dev)
+    q, k = qk_norm_rope_prefill(qkv[:, :2048].view(T, 16, 128), qkv[:, 2048:3072].view(T, 8, 128),
+                                qkv[:, 3072:].view(T, 8, 128), qw, kw, 1e-6, cos, sin, pos, None,
+                                none_pool, none_pool, 0)
+    v = qkv[:, 3072:].reshape(T, 8, 128).contiguous()
+    cu = torch.tensor([0] + list(torch.tensor(lens).cumsum(0).tolist()), dtype=torch.int32,
+                      device=dev)
     out = torch.empty_like(q)
-    mx = max(c.lens)
+    mx = max(lens)
+    scale = 128 ** -0.5
 
     def step():
-        flash_attention_prefill(q, k, v, cu, c.scale, 16, 8, 128, max_seqlen=mx, out=out)
+        flash_attention_prefill(q, k, v, cu, scale, 16, 8, 128, max_seqlen=mx, out=out)
 
     wall_ms, evt_ms = time_steps(step, args.steps, args.warmup)
-    flops = 2 * 128 * 16 * sum(L * (L + 1) for L in c.lens)
+    flops = 2 * 128 * 16 * sum(L * (L + 1) for L in lens)
     tflops = flops / (evt_ms * 1e-3) / 1e12
     log(f"prefill: {evt_ms * 1e3:.1f} us/call, {tflops:.1f} TFLOP/s")
 
-    # slot write of the same prefill into a block-16 pool (one launch)
-    kb = torch.zeros(c.num_blocks, 1, 8, 16, 128, dtype=torch.bfloat16, device=dev)
+    # slot write of the same prefill into a block-16 pool (one launch), through
+    # a seeded random slot mapping over 1.25x the blocks needed
+    nblk = (T + 15) // 16 * 5 // 4 + 1
+    kb = torch.zeros(nblk, 1, 8, 16, 128, dtype=torch.bfloat16, device=dev)
     vb = torch.zeros_like(kb)
-    sm = c.slot_mapping.to(dev)
+    sm = torch.randperm(nblk * 16, device=dev, generator=g)[:T]
     lib = _lib.load()
 
     def wstep():
         rc = lib.qwen3_kv_write_slots_bf16(
             k.data_ptr(), _lib.strides(k, (0, 1)), v.data_ptr(), _lib.strides(v, (0, 1)),
             kb.data_ptr(), _lib.strides(kb, (0, 1, 2, 3)), vb.data_ptr(),
-            _lib.strides(vb, (0, 1, 2, 3)), c.num_blocks, 0, sm.data_ptr(), sm.numel(), 8, 128,
+            _lib.strides(vb, (0, 1, 2, 3)), nblk, 0, sm.data_ptr(), sm.numel(), 8, 128,
             16, _lib.stream_of(dev))
         _lib.check(rc, "slots")
 
     w_wall, w_evt = time_steps(wstep, args.steps, args.warmup)
-    wbytes = 8 * sum(c.lens) * 8 * 128 + 8 * sum(c.lens)
-    return {"workload": f"varlen causal prefill, Qwen3-0.6B shape: 8 seqs lens={c.lens}, "
+    wbytes = 8 * T * 8 * 128 + 8 * T
+    return {"workload": f"varlen causal prefill, Qwen3-0.6B shape: 8 seqs lens={lens}, "
                         "16/8 heads, head_dim 128, bf16",
             "value": round(tflops, 2), "unit": "TFLOP/s", "ms_per_step": round(evt_ms, 5),
             "flops": flops,
@@ -253,7 +375,7 @@ def main(argv=None):
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--no-cpu-baseline", action="store_true")
-    ap.add_argument("--only", choices=["decode", "prefill"], default=None)
+    ap.add_argument("--only", choices=["decode", "prefill", "pre_attention"], default=None)
     ap.add_argument("--workload", choices=["config3", "config4"], default="config3")
     ap.add_argument("--prefill-workload", choices=["config2", "steady"], default="config2",
                     help="prefill line: the Qwen3-0.6B ragged causal batch, or 8 x 4096 tokens "
@@ -291,7 +413,7 @@ def main(argv=None):
     line = {"metric": METRIC, "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
             "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "bf16",
             "data": "synthetic (seeded N(0,1) q/K/V, seeded lengths and block tables)"}
-    if args.only != "prefill":
+    if args.only in (None, "decode"):
         res = bench_decode(args, dev)
         gbs = res["bytes"] / (res["wall_ms"] * 1e-3) / 1e9
         ach = res["bytes"] / (res["evt_ms"] * 1e-3) / 1e9
@@ -321,7 +443,18 @@ def main(argv=None):
                 "frac_hbm_peak": round(r4["bytes"] / (r4["evt_ms"] * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)}
             del r4
             torch.cuda.empty_cache()
-    if args.only != "decode":
+    if args.only in (None, "pre_attention"):
+        line["pre_attention"] = bench_pre_attention(args, dev)
+        if args.only == "pre_attention":
+            pa = line["pre_attention"]["prefill"]
+            line.update(value=pa["GB/s"], unit="GB/s", ms_per_step=pa["ms_per_step"],
+                        config={"workload": pa["workload"]},
+                        roofline={"bound": "hbm", "achieved": pa["GB/s"], "peak": HBM_PEAK_GBS,
+                                  "unit": "GB/s", "frac": pa["frac_hbm_peak"], "traffic": None})
+            print(json.dumps(line))
+            return 0
+        torch.cuda.empty_cache()
+    if args.only in (None, "prefill"):
         pf = bench_prefill(args, dev)
         if args.only == "prefill":
             line.update(value=pf["value"], unit=pf["unit"], ms_per_step=pf["ms_per_step"],

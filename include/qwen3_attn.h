@@ -34,6 +34,12 @@
  *   qwen3_varlen_prefill_bf16  <- flash_attention_prefill
  *                                 (qwen3/kernels/flash_attention_varlen.py:126-194)
  *                                 + flash_attention_varlen_kernel (:25-123)
+ *   qwen3_qk_norm_rope_decode_bf16 / _slots_bf16
+ *                              <- q_norm, k_norm, apply_rotary_pos_emb and the
+ *                                 pool write that follows them
+ *                                 (qwen3/attention.py:91-96, qwen3/norm.py:22-26,
+ *                                 qwen3/rope.py:119-135 + the decode / prefill
+ *                                 writes above), fused into one launch
  */
 #ifndef QWEN3_ATTN_H
 #define QWEN3_ATTN_H
@@ -201,6 +207,69 @@ int qwen3_varlen_prefill_bf16(const void* q, const int64_t q_strides[2],
                               int max_seqlen, int64_t total_tokens,
                               int num_heads, int num_kv_heads, int head_dim,
                               float scale, int causal, void* stream);
+
+/* ------------------------------------------------------------------------
+ * Fused pre-attention step: QK-RMSNorm + RoPE + K/V pool write.
+ *
+ * Replaces, in one launch, q_norm / k_norm (qwen3/attention.py:91-92 with
+ * qwen3/norm.py:22-26), apply_rotary_pos_emb (qwen3/attention.py:95-96,
+ * qwen3/rope.py:119-135) and the pool write that follows
+ * (update_kv_batch_triton, qwen3/kernels/paged_attention.py:292-377, for
+ * decode; PagedKVCache.update, qwen3/PagedKVcache.py:177-214, for prefill).
+ * Per head row: n = bf16((fp32(x) * rsqrt(mean(x^2) + eps)) * w);
+ * out = bf16(bf16(n * bf16(cos[pos])) + bf16(rotate_half(n) * bf16(sin[pos])))
+ * with rotate_half pairing element i with i + head_dim / 2.  V is copied to
+ * the pool unchanged.
+ *   q, k, v     (tokens, heads, head_dim) bf16 views (e.g. slices of the
+ *               fused QKV projection), strides *_strides[0..1]
+ *   q_weight, k_weight  (head_dim,) bf16 RMSNorm weights
+ *   cos_table, sin_table (table_rows, head_dim) fp32, row stride
+ *               table_row_stride (the model's RoPE tables; positions outside
+ *               [0, table_rows) give zero q/k rows and no pool write)
+ *   q_out       (tokens, num_heads, head_dim) bf16
+ *   k_cache, v_cache  pool (num_blocks, num_layers, num_kv_heads, block_size,
+ *               head_dim) with strides *_strides[0..3]; layer layer_idx
+ * Supported: head_dim 128; rows 16-byte aligned.
+ * ---------------------------------------------------------------------- */
+
+/* Decode form: token b is request row_ids[b] (NULL: b); its position is
+ * seq_lens[row] (the length before this step, the reference's decode
+ * position, qwen3/model.py:76-78) and its slot comes from the resident
+ * block table, as in qwen3_kv_write_decode_bf16. */
+int qwen3_qk_norm_rope_decode_bf16(const void* q, const int64_t q_strides[2],
+                                   const void* k, const int64_t k_strides[2],
+                                   const void* v, const int64_t v_strides[2],
+                                   const void* q_weight, const void* k_weight, float eps,
+                                   const float* cos_table, const float* sin_table,
+                                   int64_t table_row_stride, int64_t table_rows,
+                                   void* q_out, const int64_t q_out_strides[2],
+                                   void* k_cache, const int64_t k_cache_strides[4],
+                                   void* v_cache, const int64_t v_cache_strides[4],
+                                   int64_t num_blocks, int layer_idx,
+                                   const int32_t* seq_lens, const int32_t* block_table,
+                                   int64_t bt_row_stride, int64_t max_rows, int64_t max_pages,
+                                   const int32_t* row_ids, int B, int num_heads,
+                                   int num_kv_heads, int head_dim, int block_size,
+                                   void* stream);
+
+/* Slot form (prefill): token t has RoPE position positions[t] (int64) and
+ * pool slot slot_mapping[t] = block * block_size + offset (int64; negative
+ * or NULL: no pool write).  k_out (nullable) receives the normalised,
+ * rotated K for the prefill attention kernel. */
+int qwen3_qk_norm_rope_slots_bf16(const void* q, const int64_t q_strides[2],
+                                  const void* k, const int64_t k_strides[2],
+                                  const void* v, const int64_t v_strides[2],
+                                  const void* q_weight, const void* k_weight, float eps,
+                                  const float* cos_table, const float* sin_table,
+                                  int64_t table_row_stride, int64_t table_rows,
+                                  const int64_t* positions, const int64_t* slot_mapping,
+                                  void* q_out, const int64_t q_out_strides[2],
+                                  void* k_out, const int64_t k_out_strides[2],
+                                  void* k_cache, const int64_t k_cache_strides[4],
+                                  void* v_cache, const int64_t v_cache_strides[4],
+                                  int64_t num_blocks, int layer_idx, int64_t num_tokens,
+                                  int num_heads, int num_kv_heads, int head_dim,
+                                  int block_size, void* stream);
 
 #ifdef __cplusplus
 }

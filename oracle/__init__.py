@@ -25,5 +25,13 @@ live in tests/test_oracle.py):
                                table (a separate read path, get_kv) is exact;
                                untouched slots stay zero; numpy and torch
                                index paths agree bit for bit.
+  pre_attention.rope_tables    the frequency law cos/sin(pos * base^(-2i/D)) in
+                               fp64; both halves equal.
+  pre_attention.qk_norm_rope_ref  RMSNorm within one bf16 ulp of the fp64
+                               closed form; RoPE within bf16 rounding of the
+                               fp64 complex rotation of each (i, i + D/2)
+                               pair; position 0 is the identity exactly;
+                               adjacent pairing, a flipped sign, an off-by-one
+                               position and norm-after-RoPE are rejected.
 No function of this package is "parity unpinned".
 """

@@ -57,9 +57,24 @@ _SIGNATURES = {
          _vp, _i, _i, _i64,
          _i, _i, _i, ctypes.c_float, _i, _vp],
     ),
+    "qwen3_qk_norm_rope_decode_bf16": (
+        _i,
+        [_vp, _c_i64p, _vp, _c_i64p, _vp, _c_i64p, _vp, _vp, ctypes.c_float,
+         _vp, _vp, _i64, _i64,
+         _vp, _c_i64p, _vp, _c_i64p, _vp, _c_i64p, _i64, _i,
+         _vp, _vp, _i64, _i64, _i64, _vp,
+         _i, _i, _i, _i, _i, _vp],
+    ),
+    "qwen3_qk_norm_rope_slots_bf16": (
+        _i,
+        [_vp, _c_i64p, _vp, _c_i64p, _vp, _c_i64p, _vp, _vp, ctypes.c_float,
+         _vp, _vp, _i64, _i64, _vp, _vp,
+         _vp, _c_i64p, _vp, _c_i64p, _vp, _c_i64p, _vp, _c_i64p, _i64, _i,
+         _i64, _i, _i, _i, _i, _vp],
+    ),
 }
 
-ABI_VERSION = 1
+ABI_VERSION = 2
 
 _lib = None
 

@@ -97,6 +97,32 @@ def test_prefill_rejects_bad_arguments():
     assert call(qs=_s(2048, 129)) == -2
 
 
+def test_pre_attention_rejects_bad_arguments():
+    lib = _lib.load()
+    qs, ks, c4 = _s(4096, 128), _s(4096, 128), _s(1 << 16, 1 << 14, 2048, 128)
+
+    def dec(D=128, q=FAKE, q_strides=qs, tab_stride=128, bt_stride=8):
+        return lib.qwen3_qk_norm_rope_decode_bf16(
+            q, q_strides, FAKE, ks, FAKE, ks, FAKE, FAKE, 1e-6, FAKE, FAKE, tab_stride, 64,
+            FAKE, _s(2048, 128), FAKE, c4, FAKE, c4, 16, 0, FAKE, FAKE, bt_stride, 4, 8, None,
+            2, 16, 8, D, 16, None)
+
+    assert dec(D=64) == -3
+    assert dec(q=None) == -1
+    assert dec(q=FAKE + 2) == -2
+    assert dec(q_strides=_s(4100, 128)) == -2
+    assert dec(tab_stride=130) == -2
+    assert dec(bt_stride=4) == -1  # table rows shorter than max_pages
+
+    def slots(positions=FAKE, D=128):
+        return lib.qwen3_qk_norm_rope_slots_bf16(
+            FAKE, qs, FAKE, ks, FAKE, ks, FAKE, FAKE, 1e-6, FAKE, FAKE, 128, 64, positions, None,
+            FAKE, _s(2048, 128), None, None, FAKE, c4, FAKE, c4, 16, 0, 5, 16, 8, D, 16, None)
+
+    assert slots(positions=None) == -1
+    assert slots(D=256) == -3
+
+
 def test_kv_write_rejects_bad_arguments():
     lib = _lib.load()
     c4 = _s(1 << 16, 1 << 14, 2048, 128)

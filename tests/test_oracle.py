@@ -288,3 +288,89 @@ def test_slots_form_equals_range_form():
     k_pad = np.concatenate([k_new, rng.integers(0, 2 ** 16, (5, 2, 128), dtype=np.uint16)])
     ok.slots_write_ref(k_pad, k_pad, kb2, vb2, slots_pad, 0)
     assert np.array_equal(ka, kb2)
+
+
+# ---- fused pre-attention: QK-RMSNorm + RoPE --------------------------------
+
+from oracle import pre_attention as opa  # noqa: E402
+
+
+def _norm_case(T=7, H=5, seed=0):
+    g = torch.Generator().manual_seed(seed)
+    x = (torch.randn(T, H, 128, generator=g) * 3).to(torch.bfloat16)
+    w = (1 + 0.1 * torch.randn(128, generator=g)).to(torch.bfloat16)
+    return x, w
+
+
+def _rope_err(out, n, pos):
+    """Largest |out - exact rotation| over each pair's magnitude."""
+    exact = opa.rope_closed_form_fp64(n, pos, 128)
+    mag = torch.sqrt(n[..., :64].double() ** 2 + n[..., 64:].double() ** 2)
+    mag = torch.cat((mag, mag), dim=-1) + 1e-30
+    return ((out.double() - exact).abs() / mag).max().item()
+
+
+def test_rms_norm_within_one_bf16_ulp_of_fp64():
+    x, w = _norm_case()
+    got = oi.rms_norm(x, w, 1e-6).double()
+    exact = opa.rms_closed_form_fp64(x, w, 1e-6)
+    assert ((got - exact).abs() <= exact.abs() * 2.0 ** -8 + 1e-30).all()
+    # a plausible mistake: forgetting the weight, or the eps inside the mean
+    assert not ((x.double() / torch.sqrt(x.double().pow(2).mean(-1, keepdim=True))
+                 - exact).abs() <= exact.abs() * 2.0 ** -8).all()
+
+
+def test_rope_tables_follow_the_frequency_law():
+    cos, sin = opa.rope_tables(128, 1e6, 64)
+    pos = torch.arange(64, dtype=torch.float64)[:, None]
+    theta = 1e6 ** (-torch.arange(64, dtype=torch.float64) / 64)
+    ang = pos * theta[None, :]
+    # fp32 angles pos * inv_freq carry up to ~63 * 2^-24 of rounding
+    assert torch.allclose(cos[:, :64].double(), torch.cos(ang), atol=2e-5)
+    assert torch.allclose(sin[:, 64:].double(), torch.sin(ang), atol=2e-5)
+    # and a wrong frequency law (base^(-i/D) instead of base^(-2i/D)) is far off
+    assert not torch.allclose(cos[:, :64].double(),
+                              torch.cos(pos * (1e6 ** (-torch.arange(64, dtype=torch.float64) / 128))),
+                              atol=1e-2)
+    assert torch.equal(cos[:, :64], cos[:, 64:]) and torch.equal(sin[:, :64], sin[:, 64:])
+
+
+def test_rope_is_the_complex_rotation_within_bf16():
+    x, w = _norm_case(T=9)
+    n = oi.rms_norm(x, w, 1e-6)
+    cos, sin = opa.rope_tables(128, 1e6, 4096)
+    pos = torch.tensor([0, 1, 2, 7, 100, 513, 1024, 2047, 4095])
+    out = oi.apply_rope(n, cos[pos], sin[pos])
+    assert _rope_err(out, n, pos) < 2.0 ** -6
+    # position 0 is the identity, exactly
+    assert torch.equal(out[0], n[0])
+
+
+def test_rope_closed_form_rejects_planted_mistakes():
+    x, w = _norm_case(T=9, seed=1)
+    n = oi.rms_norm(x, w, 1e-6)
+    cos, sin = opa.rope_tables(128, 1e6, 4096)
+    pos = torch.tensor([3, 5, 9, 33, 100, 513, 1024, 2047, 4000])
+    c, s = cos[pos][:, None, :], sin[pos][:, None, :]
+    nf = n.float()
+    # adjacent pairs (2i, 2i+1) instead of (i, i + D/2)
+    adj = torch.stack((-nf[..., 1::2], nf[..., 0::2]), dim=-1).reshape(nf.shape)
+    assert _rope_err((nf * c + adj * s).to(torch.bfloat16), n, pos) > 0.05
+    # rotate_half with the sign on the wrong half
+    bad = torch.cat((nf[..., 64:], -nf[..., :64]), dim=-1)
+    assert _rope_err((nf * c + bad * s).to(torch.bfloat16), n, pos) > 0.05
+    # position off by one
+    assert _rope_err(oi.apply_rope(n, cos[pos + 1], sin[pos + 1]), n, pos) > 0.05
+    # normalising after the rotation (the weight then multiplies rotated pairs)
+    late = oi.rms_norm(oi.apply_rope(x, cos[pos], sin[pos]), w, 1e-6)
+    assert _rope_err(late, n, pos) > 0.05
+
+
+def test_qk_norm_rope_ref_composes_the_two_steps():
+    x, w = _norm_case(T=4, H=6)
+    kx, kw = _norm_case(T=4, H=2, seed=3)
+    cos, sin = opa.rope_tables(128, 1e6, 64)
+    pos = torch.tensor([0, 5, 17, 63])
+    q, k = opa.qk_norm_rope_ref(x, kx, w, kw, 1e-6, cos, sin, pos)
+    assert torch.equal(q, oi.apply_rope(oi.rms_norm(x, w, 1e-6), cos[pos], sin[pos]))
+    assert _rope_err(k, oi.rms_norm(kx, kw, 1e-6), pos) < 2.0 ** -6
