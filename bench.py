@@ -180,6 +180,7 @@ def cpu_baseline_decode(res, n_seq=64):
 
 PROFILE_DIR = Path(__file__).resolve().parent / "profiles"
 TRAFFIC_PROFILE = "paged_decode_stream_b256_qwen3_8b.md"
+PRE_ATTENTION_PROFILE = "pre_attention_qwen3.md"
 
 
 def profiled_traffic(name: str):
@@ -234,7 +235,9 @@ def bench_pre_attention(args, dev):
     log(f"pre-attention (prefill, {T} tokens): {p_evt * 1e3:.1f} us/call, {gbs:.0f} GB/s")
     res["prefill"] = {"workload": f"Qwen3-0.6B prefill batch, {T} tokens, 16/8 heads",
                       "ms_per_step": round(p_evt, 5), "bytes": pbytes, "GB/s": round(gbs, 1),
-                      "frac_hbm_peak": round(gbs / HBM_PEAK_GBS, 4)}
+                      "frac_hbm_peak": round(gbs / HBM_PEAK_GBS, 4),
+                      "traffic": profiled_traffic(PRE_ATTENTION_PROFILE),
+                      "traffic_source": f"profiles/{PRE_ATTENTION_PROFILE}"}
     del qkv, q, k, v, kb, vb, qo, ko
 
     from qwen3_engine_from_scratch_amd.PagedKVcache import KVCachePool
@@ -450,7 +453,8 @@ def main(argv=None):
             line.update(value=pa["GB/s"], unit="GB/s", ms_per_step=pa["ms_per_step"],
                         config={"workload": pa["workload"]},
                         roofline={"bound": "hbm", "achieved": pa["GB/s"], "peak": HBM_PEAK_GBS,
-                                  "unit": "GB/s", "frac": pa["frac_hbm_peak"], "traffic": None})
+                                  "unit": "GB/s", "frac": pa["frac_hbm_peak"],
+                                  "traffic": pa["traffic"]})
             print(json.dumps(line))
             return 0
         torch.cuda.empty_cache()
