@@ -1,7 +1,7 @@
 """Benchmark of the MI355X attention hot path.
 
     python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu-baseline]
-                    [--only decode|prefill] [--workload config3|config4]
+                    [--only decode|prefill|pre_attention|e2e] [--workload config3|config4]
 
 Headline (the JSON `value`): paged decode attention at the Qwen3-8B shape —
 batch 256, 32 query / 8 KV heads, head_dim 128, bf16, block 16, context
@@ -18,7 +18,12 @@ Also reported on the same line:
                 bounded sample (the first 64 sequences) of the same workload;
   prefill       varlen causal prefill at the Qwen3-0.6B shape (8 sequences,
                 lengths uniform in [64, 2048], 16/8 heads) in TFLOP/s against
-                the 2.5 PFLOP/s bf16 dense MFMA peak, plus its slot write.
+                the 2.5 PFLOP/s bf16 dense MFMA peak, plus its slot write;
+  pre_attention the fused QK-RMSNorm + RoPE + pool write (prefill and decode
+                forms) against the HBM peak;
+  e2e           the whole Qwen3-0.6B model (random-init bf16) serving 64
+                requests by continuous batching, 256 greedy tokens each, in
+                output tokens/s.
 Prints exactly one JSON line on stdout (progress goes to stderr).
 """
 from __future__ import annotations
@@ -372,13 +377,80 @@ def bench_prefill(args, dev):
                            "ms_per_step": round(w_evt, 5), "bytes": wbytes}}
 
 
+def bench_e2e(args, dev):
+    """Whole Qwen3-0.6B (random-init bf16 weights) serving 64 requests with
+    continuous batching: prompts of seeded lengths uniform in [128, 1024],
+    256 greedy tokens each (the first from the prefill), prefill through the
+    varlen kernel, decode through captured graphs per power-of-two bucket.
+    Reports output tokens/s over the whole run (prefill included), after an
+    untimed warm-up run of the same requests with 4 tokens each."""
+    import random
+
+    import torch
+
+    from qwen3_engine_from_scratch_amd.PagedKVcache import KVCachePool
+    from qwen3_engine_from_scratch_amd.config import qwen3_0p6b_config
+    from qwen3_engine_from_scratch_amd.engine import Engine, GenRequest
+    from qwen3_engine_from_scratch_amd.model import Qwen3ForCausalLM, init_random_weights
+
+    n_req, lo, hi, new_tokens = 64, 128, 1024, args.e2e_tokens
+    cfg = qwen3_0p6b_config(max_position_embeddings=4096)
+    t0 = time.perf_counter()
+    with torch.device(dev):
+        model = Qwen3ForCausalLM(cfg)
+    init_random_weights(model, seed=0)
+    model = model.to(torch.bfloat16).eval()
+    rng = random.Random(0)
+    lens = [rng.randint(lo, hi) for _ in range(n_req)]
+    g = torch.Generator().manual_seed(0)
+    prompts = [torch.randint(0, cfg.vocab_size, (L,), generator=g).tolist() for L in lens]
+    bs = 16
+    max_seq = hi + new_tokens
+    blocks = n_req * ((max_seq + bs - 1) // bs) + n_req + 1 + 16
+    pool = KVCachePool(blocks, cfg.num_hidden_layers, bs, cfg.num_key_value_heads, cfg.head_dim,
+                       device=dev, dtype=torch.bfloat16, max_seq_len=max_seq,
+                       max_requests=2 * n_req + 8)
+    t1 = time.perf_counter()
+    engine = Engine(model, pool, max_batch=n_req, use_graph=True)
+    torch.cuda.synchronize()
+    t2 = time.perf_counter()
+    log(f"e2e: model init {t1 - t0:.1f} s, graph capture {t2 - t1:.1f} s")
+    engine.generate([GenRequest(i, p, 4) for i, p in enumerate(prompts)])
+    torch.cuda.synchronize()
+    reqs = [GenRequest(i, p, new_tokens) for i, p in enumerate(prompts)]
+    st = engine.generate(reqs)
+    engine.close()
+    dec_steps = max(st["decode_steps"], 1)
+    log(f"e2e: {st['output_tokens']} tokens in {st['total_s']:.3f} s = "
+        f"{st['tokens_per_s']:.0f} tok/s (prefill {st['prefill_s'] * 1e3:.1f} ms, "
+        f"decode {st['decode_s'] * 1e3 / dec_steps:.3f} ms/step over {dec_steps} steps)")
+    # bytes one decode step must read at the final context length: the weights
+    # (the tied embedding once, as lm_head) and every live K/V token
+    n_w = sum(p.numel() for p in model.parameters())
+    ctx = sum(lens) + n_req * new_tokens
+    kv_step = ctx * cfg.num_hidden_layers * cfg.num_key_value_heads * cfg.head_dim * 2 * 2
+    return {"metric": "output tokens/s", "value": round(st["tokens_per_s"], 1),
+            "unit": "tokens/s",
+            "workload": "Qwen3-0.6B random-init bf16, 64 requests, prompts U[128,1024] "
+                        f"(sum {sum(lens)}), {new_tokens} greedy tokens each, max batch 64, "
+                        "decode in captured graphs (buckets 1..64)",
+            "total_s": round(st["total_s"], 4), "output_tokens": st["output_tokens"],
+            "prefill_ms": round(st["prefill_s"] * 1e3, 2),
+            "decode_ms_per_step": round(st["decode_s"] * 1e3 / dec_steps, 4),
+            "decode_steps": st["decode_steps"], "prefill_steps": st["prefill_steps"],
+            "weight_bytes": 2 * n_w, "kv_bytes_last_step": kv_step}
+
+
 def main(argv=None):
     ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--no-cpu-baseline", action="store_true")
-    ap.add_argument("--only", choices=["decode", "prefill", "pre_attention"], default=None)
+    ap.add_argument("--only", choices=["decode", "prefill", "pre_attention", "e2e"],
+                    default=None)
+    ap.add_argument("--e2e-tokens", type=int, default=256,
+                    help="greedy tokens per request in the whole-model serving line")
     ap.add_argument("--workload", choices=["config3", "config4"], default="config3")
     ap.add_argument("--prefill-workload", choices=["config2", "steady"], default="config2",
                     help="prefill line: the Qwen3-0.6B ragged causal batch, or 8 x 4096 tokens "
@@ -464,6 +536,13 @@ def main(argv=None):
             line.update(value=pf["value"], unit=pf["unit"], ms_per_step=pf["ms_per_step"],
                         config={"workload": pf["workload"]}, roofline=pf["roofline"])
         line["prefill"] = pf
+        torch.cuda.empty_cache()
+    if args.only in (None, "e2e"):
+        e2e = bench_e2e(args, dev)
+        if args.only == "e2e":
+            line.update(value=e2e["value"], unit=e2e["unit"],
+                        ms_per_step=e2e["decode_ms_per_step"], config={"workload": e2e["workload"]})
+        line["e2e"] = e2e
     print(json.dumps(line))
     return 0
 

@@ -232,10 +232,13 @@ int qwen3_varlen_prefill_bf16(const void* q, const int64_t q_strides[2],
  * Supported: head_dim 128; rows 16-byte aligned.
  * ---------------------------------------------------------------------- */
 
-/* Decode form: token b is request row_ids[b] (NULL: b); its position is
- * seq_lens[row] (the length before this step, the reference's decode
- * position, qwen3/model.py:76-78) and its slot comes from the resident
- * block table, as in qwen3_kv_write_decode_bf16. */
+/* Decode form: token b is request row_ids[b] (NULL: b); it is written at
+ * position seq_lens[row] (the length before this step) through the resident
+ * block table, as in qwen3_kv_write_decode_bf16, and rotated at
+ * positions[b] (int64), the position_ids the reference passes
+ * (qwen3/model.py:76-78, qwen3/graph_runner.py:190, bench_batched.py:182); positions NULL:
+ * rotated at seq_lens[row] too, which is what every reference driver
+ * passes. */
 int qwen3_qk_norm_rope_decode_bf16(const void* q, const int64_t q_strides[2],
                                    const void* k, const int64_t k_strides[2],
                                    const void* v, const int64_t v_strides[2],
@@ -248,9 +251,9 @@ int qwen3_qk_norm_rope_decode_bf16(const void* q, const int64_t q_strides[2],
                                    int64_t num_blocks, int layer_idx,
                                    const int32_t* seq_lens, const int32_t* block_table,
                                    int64_t bt_row_stride, int64_t max_rows, int64_t max_pages,
-                                   const int32_t* row_ids, int B, int num_heads,
-                                   int num_kv_heads, int head_dim, int block_size,
-                                   void* stream);
+                                   const int32_t* row_ids, const int64_t* positions, int B,
+                                   int num_heads, int num_kv_heads, int head_dim,
+                                   int block_size, void* stream);
 
 /* Slot form (prefill): token t has RoPE position positions[t] (int64) and
  * pool slot slot_mapping[t] = block * block_size + offset (int64; negative

@@ -21,7 +21,8 @@ import torch
 from . import _lib
 from .kernels.paged_attention import update_kv_batch_hip
 
-__all__ = ["KVCachePool", "PagedKVCache", "prefill_slot_mapping", "write_prefill_batch"]
+__all__ = ["KVCachePool", "PagedKVCache", "prefill_slot_mapping", "write_prefill_batch",
+           "reserve_pages_bulk", "set_seq_lens_bulk"]
 
 
 class KVCachePool:
@@ -170,6 +171,20 @@ class PagedKVCache:
             _lib.stream_of(dev))
         _lib.check(rc, "qwen3_kv_write_range_bf16")
 
+    def reserve_slots(self, n: int):
+        """Reserves the pages of positions seq_len .. seq_len + n - 1 (as
+        update does, :186-190) and returns their pool slots, block *
+        block_size + offset, as an int64 numpy array."""
+        import numpy as np
+
+        bs = self._pool.block_size
+        end = self.seq_len + n
+        while len(self.block_table) < (end + bs - 1) // bs:
+            self._allocate_block()
+        p = np.arange(self.seq_len, end, dtype=np.int64)
+        table = np.asarray(self.block_table, dtype=np.int64)
+        return table[p // bs] * bs + p % bs
+
     def advance_seq_len(self, n: int = 1):
         self.seq_len += n
         self._pool.seq_lens[self.row_id] = self.seq_len
@@ -181,6 +196,46 @@ class PagedKVCache:
             self.num_pages = 0
         self.seq_len = 0
         self._pool.free_row(self.row_id)
+
+
+def reserve_pages_bulk(caches, tokens: list) -> None:
+    """Gives every handle enough pages for tokens[i] tokens with one pool
+    allocation (one zeroing launch) and one block-table write for the whole
+    batch, instead of a device write per page (_allocate_block).  Used by the
+    batching engine once per step."""
+    pool = caches[0]._pool
+    bs = pool.block_size
+    max_pages = pool.block_table_2d.shape[1]
+    want = []
+    for c, n in zip(caches, tokens):
+        k = (int(n) + bs - 1) // bs - c.num_pages
+        if k > 0:
+            assert c.num_pages + k <= max_pages, \
+                f"request exceeds max_seq_len ({pool.max_seq_len} tokens / {max_pages} pages)"
+            want.append((c, k))
+    total = sum(k for _, k in want)
+    if total == 0:
+        return
+    ids = pool.alloc(total)
+    rows, cols, vals = [], [], []
+    for c, k in want:
+        new, ids = ids[:k], ids[k:]
+        rows += [c.row_id] * k
+        cols += range(c.num_pages, c.num_pages + k)
+        vals += new
+        c.block_table.extend(new)
+        c.num_pages += k
+    idx = torch.tensor([rows, cols, vals], dtype=torch.int64).to(pool.block_table_2d.device)
+    pool.block_table_2d.index_put_((idx[0], idx[1]), idx[2].to(torch.int32))
+
+
+def set_seq_lens_bulk(caches) -> None:
+    """Writes every handle's host seq_len into the resident seq_lens table
+    with one copy (the batched form of advance_seq_len's device write)."""
+    pool = caches[0]._pool
+    idx = torch.tensor([[c.row_id for c in caches], [c.seq_len for c in caches]],
+                       dtype=torch.int64).to(pool.seq_lens.device)
+    pool.seq_lens.index_put_((idx[0],), idx[1].to(torch.int32))
 
 
 def prefill_slot_mapping(caches, S: int, device) -> torch.Tensor:

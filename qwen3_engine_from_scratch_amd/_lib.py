@@ -62,7 +62,7 @@ _SIGNATURES = {
         [_vp, _c_i64p, _vp, _c_i64p, _vp, _c_i64p, _vp, _vp, ctypes.c_float,
          _vp, _vp, _i64, _i64,
          _vp, _c_i64p, _vp, _c_i64p, _vp, _c_i64p, _i64, _i,
-         _vp, _vp, _i64, _i64, _i64, _vp,
+         _vp, _vp, _i64, _i64, _i64, _vp, _vp,
          _i, _i, _i, _i, _i, _vp],
     ),
     "qwen3_qk_norm_rope_slots_bf16": (
@@ -72,9 +72,18 @@ _SIGNATURES = {
          _vp, _c_i64p, _vp, _c_i64p, _vp, _c_i64p, _vp, _c_i64p, _i64, _i,
          _i64, _i, _i, _i, _i, _vp],
     ),
+    # include/qwen3_model_ops.h
+    "qwen3_add_rms_norm_bf16": (
+        _i,
+        [_vp, _i64, _vp, _i64, _vp, _i64, _vp, ctypes.c_float, _vp, _i64,
+         _vp, _i64, _i64, _i, _vp],
+    ),
+    "qwen3_silu_mul_bf16": (_i, [_vp, _i64, _vp, _i64, _i64, _i, _vp]),
+    "qwen3_argmax_bf16": (_i, [_vp, _i64, _i64, _i64, _vp, _vp]),
+    "qwen3_advance_seq_lens": (_i, [_vp, _i64, _vp, _i, _i, _i, _vp]),
 }
 
-ABI_VERSION = 2
+ABI_VERSION = 3
 
 _lib = None
 

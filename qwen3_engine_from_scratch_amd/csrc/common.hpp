@@ -6,6 +6,7 @@
 #include <stdint.h>
 
 #include "qwen3_attn.h"
+#include "qwen3_model_ops.h"
 
 namespace q3 {
 

@@ -55,6 +55,7 @@ struct PreAttnArgs {
   const int32_t* block_table;
   int64_t bt_stride, max_rows, max_pages;
   const int32_t* row_ids;  // nullable: identity
+  const int64_t* rope_pos;  // nullable: RoPE at the write position seq_lens[row]
   // Slots addressing: explicit position and slot per token (slot < 0: no write).
   const int64_t* positions;
   const int64_t* slots;
@@ -108,12 +109,13 @@ __global__ __launch_bounds__(256) void pre_attention_kernel(PreAttnArgs a) {
   if constexpr (A == Addr::Decode) {
     const int64_t row = a.row_ids ? a.row_ids[t] : t;
     if (row >= 0 && row < a.max_rows) {
-      pos = a.seq_lens[row];
-      const int64_t pg = pos >= 0 ? pos / a.bs : -1;
+      const int64_t wpos = a.seq_lens[row];
+      const int64_t pg = wpos >= 0 ? wpos / a.bs : -1;
       if (pg >= 0 && pg < a.max_pages) {
         phys = a.block_table[row * a.bt_stride + pg];
-        off = pos % a.bs;
+        off = wpos % a.bs;
       }
+      pos = a.rope_pos ? a.rope_pos[t] : wpos;
     }
   } else {
     pos = a.positions[t];
@@ -299,8 +301,9 @@ extern "C" int qwen3_qk_norm_rope_decode_bf16(
     int64_t table_rows, void* q_out, const int64_t q_out_strides[2], void* k_cache,
     const int64_t k_cache_strides[4], void* v_cache, const int64_t v_cache_strides[4],
     int64_t num_blocks, int layer_idx, const int32_t* seq_lens, const int32_t* block_table,
-    int64_t bt_row_stride, int64_t max_rows, int64_t max_pages, const int32_t* row_ids, int B,
-    int num_heads, int num_kv_heads, int head_dim, int block_size, void* stream) {
+    int64_t bt_row_stride, int64_t max_rows, int64_t max_pages, const int32_t* row_ids,
+    const int64_t* positions, int B, int num_heads, int num_kv_heads, int head_dim,
+    int block_size, void* stream) {
   const char* who = "qwen3_qk_norm_rope_decode_bf16";
   if (!q_strides || !k_strides || !v_strides || !q_out_strides || !k_cache_strides ||
       !v_cache_strides || !seq_lens || !block_table)
@@ -318,6 +321,7 @@ extern "C" int qwen3_qk_norm_rope_decode_bf16(
   a.max_rows = max_rows;
   a.max_pages = max_pages;
   a.row_ids = row_ids;
+  a.rope_pos = positions;
   a.n_tokens = B;
   if (int rc = check_args(a, head_dim, who)) return rc;
   return launch<Addr::Decode>(a, stream, who);

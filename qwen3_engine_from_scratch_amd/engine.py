@@ -1,0 +1,188 @@
+"""Continuous-batching generation loop over the HIP model steps.
+
+Scheduling policy is the reference's (qwen3/scheduler.py:56-97): while the
+running set has free slots and requests wait, the step is a prefill of as
+many waiting requests as fit; otherwise it is a decode step of every running
+request.  A request finishes after max_new_tokens tokens (the first comes
+from its prefill) or on its eos token, and returns its pages.
+
+What differs from the reference's driver (bench_batched.py:139-203) is where
+the per-step state lives:
+  - prefill packs the prompts (varlen kernel, no padding) and computes
+    logits only for each prompt's last token;
+  - decode steps replay a captured graph per power-of-two bucket whose
+    greedy tokens are written straight into the next step's inputs and
+    whose resident seq_lens advance on the device, so an unchanged batch
+    needs no host->device copy at all; a changed batch copies its ids and
+    rows once;
+  - pages for the next token are reserved for the whole batch with one pool
+    allocation and one block-table write (reserve_pages_bulk);
+  - the host reads back only the B new token ids per step.
+Greedy decoding only (temperature 0), as the reference's benchmark runs.
+"""
+from __future__ import annotations
+
+import time
+from collections import deque
+from dataclasses import dataclass, field
+
+import numpy as np
+import torch
+
+from .PagedKVcache import PagedKVCache, reserve_pages_bulk, set_seq_lens_bulk
+from .graph_runner import GraphRunner, pow2_buckets
+from .kernels.model_ops import argmax
+
+__all__ = ["GenRequest", "Engine"]
+
+
+@dataclass
+class GenRequest:
+    """One generation request (the data half of qwen3/request.py:44-206)."""
+    request_id: int
+    prompt: list
+    max_new_tokens: int
+    eos_token_id: int | None = None
+    output_ids: list = field(default_factory=list)
+    cache: PagedKVCache | None = None
+    finished: bool = False
+    finish_time: float = 0.0
+
+    def is_finished(self) -> bool:
+        return (len(self.output_ids) >= self.max_new_tokens
+                or (self.eos_token_id is not None and bool(self.output_ids)
+                    and self.output_ids[-1] == self.eos_token_id))
+
+
+class Engine:
+    def __init__(self, model, pool, max_batch: int = 64, use_graph: bool = True):
+        self.model = model
+        self.pool = pool
+        self.max_batch = max_batch
+        self.device = pool.k_buffer.device
+        self.runner = None
+        self._placeholders = []
+        if use_graph:
+            buckets = pow2_buckets(max_batch)
+            self._placeholders = [PagedKVCache(pool) for _ in range(max(buckets))]
+            self.runner = GraphRunner(model, pool, self._placeholders, buckets, reserve_pages=1,
+                                      greedy=True, advance=True, positions_from_lengths=True)
+        else:
+            model.reserve_decode_workspace(max_batch, pool)
+        self._tok_host = torch.empty(max(max_batch, 1), dtype=torch.int64, pin_memory=True)
+        self._last_batch = None  # (bucket, tuple of request ids) of the last graph replay
+
+    # ---- steps -------------------------------------------------------------
+
+    def _prefill(self, reqs) -> None:
+        dev = self.device
+        lens = [len(r.prompt) for r in reqs]
+        for r in reqs:
+            r.cache = PagedKVCache(self.pool)
+        reserve_pages_bulk([r.cache for r in reqs], lens)
+        n = len(reqs)
+        cu = np.zeros(n + 1, dtype=np.int64)
+        cu[1:] = np.cumsum(lens)
+        T = int(cu[-1])
+        bs = self.pool.block_size
+        # one host buffer, one copy: ids | positions | slots | last rows | cu
+        buf = np.empty(3 * T + 2 * n + 1, dtype=np.int64)
+        buf[:T] = np.concatenate([np.asarray(r.prompt, dtype=np.int64) for r in reqs])
+        buf[T:2 * T] = np.concatenate([np.arange(L, dtype=np.int64) for L in lens])
+        slots = buf[2 * T:3 * T]
+        for r, a, L in zip(reqs, cu[:-1], lens):
+            p = np.arange(L, dtype=np.int64)
+            table = np.asarray(r.cache.block_table, dtype=np.int64)
+            slots[a:a + L] = table[p // bs] * bs + p % bs
+        buf[3 * T:3 * T + n] = cu[1:] - 1
+        buf[3 * T + n:] = cu
+        d = torch.from_numpy(buf).to(dev)
+        logits = self.model.prefill_logits(d[:T], d[3 * T + n:].to(torch.int32), max(lens),
+                                           d[T:2 * T], d[2 * T:3 * T], self.pool,
+                                           d[3 * T:3 * T + n])
+        toks = argmax(logits).cpu().tolist()
+        for r, L, tok in zip(reqs, lens, toks):
+            r.cache.seq_len = L
+            r.output_ids.append(int(tok))
+        set_seq_lens_bulk([r.cache for r in reqs])
+
+    def _decode(self, reqs) -> None:
+        k = len(reqs)
+        caches = [r.cache for r in reqs]
+        # the token of this step lands at position seq_len: reserve its page
+        reserve_pages_bulk(caches, [c.seq_len + 1 for c in caches])
+        dev = self.device
+        if self.runner is not None:
+            b = self.runner.bucket_for(k)
+            key = (b, tuple(r.request_id for r in reqs))
+            if key == self._last_batch:
+                out = self.runner.replay_greedy(k)
+            else:
+                ids = torch.tensor([r.output_ids[-1] for r in reqs], dtype=torch.int64)
+                rows = torch.tensor([c.row_id for c in caches], dtype=torch.int32)
+                out = self.runner.replay_greedy(k, ids.to(dev), rows.to(dev))
+                self._last_batch = key
+            toks = out.view(-1)[:k]
+        else:
+            ids = torch.tensor([r.output_ids[-1] for r in reqs], dtype=torch.int64).to(dev)
+            rows = torch.tensor([c.row_id for c in caches], dtype=torch.int32).to(dev)
+            logits = self.model.decode_logits(ids, rows, self.pool)
+            toks = argmax(logits)
+        host = self._tok_host[:k]
+        host.copy_(toks, non_blocking=True)
+        torch.cuda.current_stream(dev).synchronize()
+        for c in caches:
+            c.seq_len += 1
+        if self.runner is None:
+            set_seq_lens_bulk(caches)
+        for r, tok in zip(reqs, host.tolist()):
+            r.output_ids.append(int(tok))
+
+    # ---- loop --------------------------------------------------------------
+
+    @torch.no_grad()
+    def generate(self, requests: list) -> dict:
+        """Runs every request to completion; returns timing and counts."""
+        waiting = deque(requests)
+        running: list = []
+        t0 = time.perf_counter()
+        prefill_s = decode_s = 0.0
+        n_prefill = n_decode = 0
+        while waiting or running:
+            ts = time.perf_counter()
+            if waiting and len(running) < self.max_batch:
+                take = [waiting.popleft()
+                        for _ in range(min(self.max_batch - len(running), len(waiting)))]
+                self._prefill(take)
+                running.extend(take)
+                batch, is_prefill = take, True
+            else:
+                batch, is_prefill = running[:self.max_batch], False
+                self._decode(batch)
+            dt = time.perf_counter() - ts
+            if is_prefill:
+                prefill_s += dt
+                n_prefill += 1
+            else:
+                decode_s += dt
+                n_decode += 1
+            done = [r for r in batch if r.is_finished()]
+            if done:
+                now = time.perf_counter() - t0
+                for r in done:
+                    r.finished = True
+                    r.finish_time = now
+                    r.cache.free()
+                    r.cache = None
+                running = [r for r in running if not r.finished]
+        total = time.perf_counter() - t0
+        n_tok = sum(len(r.output_ids) for r in requests)
+        return {"total_s": total, "output_tokens": n_tok, "tokens_per_s": n_tok / total,
+                "prefill_s": prefill_s, "decode_s": decode_s, "prefill_steps": n_prefill,
+                "decode_steps": n_decode}
+
+    def close(self):
+        if self.runner is not None:
+            self.runner.free()
+        for c in self._placeholders:
+            c.free()

@@ -1,0 +1,124 @@
+"""Row-wise kernels around the attention path of a Qwen3 decoder step, on
+the gfx950 HIP library (include/qwen3_model_ops.h): residual add + RMSNorm
+(also the embedding lookup and the final-norm row selection), SwiGLU
+activation, greedy token choice and the resident-length advance.
+
+Reference modules: qwen3/norm.py:22-26, qwen3/decoder.py:49,55,
+qwen3/mlp.py:31-36, qwen3/sampling.py:256-258, qwen3/PagedKVcache.py:216-219.
+"""
+from __future__ import annotations
+
+import torch
+
+from .. import _lib
+
+__all__ = ["add_rms_norm", "embed_rms_norm", "silu_mul", "argmax", "advance_seq_lens"]
+
+
+def _rows2d(t: torch.Tensor) -> torch.Tensor:
+    assert t.dim() == 2 and t.stride(1) == 1, "expected a (rows, hidden) row-major view"
+    return t
+
+
+def add_rms_norm(x: torch.Tensor | None, residual: torch.Tensor, weight: torch.Tensor,
+                 eps: float, *, residual_out: torch.Tensor | None = None,
+                 out: torch.Tensor | None = None,
+                 row_index: torch.Tensor | None = None) -> torch.Tensor:
+    """h = residual + x (bf16; x None: h = residual), out = RMSNorm(h) * weight;
+    h is stored in `residual_out` when given (pass `residual` itself for the
+    in-place residual-stream update of a decoder layer).
+
+    row_index (int64, optional): output row i reads source row row_index[i]
+    (the final norm over the last token of each packed sequence).
+    Returns `out` (rows, hidden) bf16.
+    """
+    residual = _rows2d(residual)
+    if x is not None:
+        x = _rows2d(x)
+        assert x.shape == residual.shape
+    hidden = residual.shape[1]
+    if row_index is not None:
+        assert row_index.dtype == torch.int64
+        row_index = row_index.reshape(-1).contiguous()
+        rows = row_index.numel()
+    else:
+        rows = residual.shape[0]
+    assert weight.dtype == residual.dtype == torch.bfloat16 and weight.is_contiguous()
+    dev = _lib.require_hip(x, residual, weight, residual_out, out, row_index)
+    if out is None:
+        out = torch.empty(rows, hidden, dtype=residual.dtype, device=residual.device)
+    _rows2d(out)
+    if residual_out is not None:
+        _rows2d(residual_out)
+        assert residual_out.shape == (rows, hidden)
+    rc = _lib.load().qwen3_add_rms_norm_bf16(
+        _lib.ptr(x), x.stride(0) if x is not None else 0,
+        residual.data_ptr(), residual.stride(0),
+        _lib.ptr(residual_out), residual_out.stride(0) if residual_out is not None else 0,
+        weight.data_ptr(), float(eps), out.data_ptr(), out.stride(0),
+        _lib.ptr(row_index), residual.shape[0], rows, hidden, _lib.stream_of(dev))
+    _lib.check(rc, "qwen3_add_rms_norm_bf16")
+    return out
+
+
+def embed_rms_norm(ids: torch.Tensor, embed_weight: torch.Tensor, norm_weight: torch.Tensor,
+                   eps: float, *, hidden_out: torch.Tensor | None = None,
+                   out: torch.Tensor | None = None) -> tuple[torch.Tensor, torch.Tensor]:
+    """Embedding lookup fused with layer 0's input RMSNorm: returns
+    (hidden, normed), both (tokens, hidden) bf16.  ids: int64 token ids; an
+    id outside the vocabulary gives zero rows."""
+    ids = ids.reshape(-1)
+    assert ids.dtype == torch.int64
+    n = ids.numel()
+    H = embed_weight.shape[1]
+    if hidden_out is None:
+        hidden_out = torch.empty(n, H, dtype=embed_weight.dtype, device=embed_weight.device)
+    out = add_rms_norm(None, embed_weight, norm_weight, eps, residual_out=hidden_out, out=out,
+                       row_index=ids)
+    return hidden_out, out
+
+
+def silu_mul(gate_up: torch.Tensor, out: torch.Tensor | None = None) -> torch.Tensor:
+    """SwiGLU activation of the fused gate/up projection (rows, 2*I) ->
+    (rows, I): bf16(bf16(silu(gate)) * up)."""
+    gate_up = _rows2d(gate_up)
+    rows, two_i = gate_up.shape
+    assert two_i % 2 == 0 and gate_up.dtype == torch.bfloat16
+    inter = two_i // 2
+    dev = _lib.require_hip(gate_up, out)
+    if out is None:
+        out = torch.empty(rows, inter, dtype=gate_up.dtype, device=gate_up.device)
+    _rows2d(out)
+    rc = _lib.load().qwen3_silu_mul_bf16(gate_up.data_ptr(), gate_up.stride(0), out.data_ptr(),
+                                         out.stride(0), rows, inter, _lib.stream_of(dev))
+    _lib.check(rc, "qwen3_silu_mul_bf16")
+    return out
+
+
+def argmax(logits: torch.Tensor, out: torch.Tensor | None = None) -> torch.Tensor:
+    """Greedy choice over (rows, vocab) bf16 logits -> (rows,) int64: the
+    first index of the maximum, NaN ranking highest (torch.argmax's rule)."""
+    logits = _rows2d(logits)
+    assert logits.dtype == torch.bfloat16
+    rows, vocab = logits.shape
+    dev = _lib.require_hip(logits, out)
+    if out is None:
+        out = torch.empty(rows, dtype=torch.int64, device=logits.device)
+    assert out.dtype == torch.int64 and out.is_contiguous() and out.numel() == rows
+    rc = _lib.load().qwen3_argmax_bf16(logits.data_ptr(), logits.stride(0), rows, vocab,
+                                       out.data_ptr(), _lib.stream_of(dev))
+    _lib.check(rc, "qwen3_argmax_bf16")
+    return out
+
+
+def advance_seq_lens(seq_lens: torch.Tensor, row_ids: torch.Tensor, skip_row: int = -1,
+                     delta: int = 1) -> None:
+    """seq_lens[row_ids[i]] += delta on the device, except rows equal to
+    skip_row; listed rows other than skip_row must be distinct."""
+    assert seq_lens.dtype == torch.int32 and seq_lens.is_contiguous()
+    assert row_ids.dtype == torch.int32 and row_ids.is_contiguous()
+    dev = _lib.require_hip(seq_lens, row_ids)
+    rc = _lib.load().qwen3_advance_seq_lens(seq_lens.data_ptr(), seq_lens.numel(),
+                                            row_ids.data_ptr(), row_ids.numel(), int(skip_row),
+                                            int(delta), _lib.stream_of(dev))
+    _lib.check(rc, "qwen3_advance_seq_lens")

@@ -24,8 +24,9 @@ def rope_tables(head_dim: int, base: float = 1e6, max_seq_len: int = 4096, devic
     base^(-2i/head_dim), their outer product with the positions, repeated
     for both halves.  Computed on the CPU (like the reference's buffers) and
     moved to `device`."""
-    inv_freq = 1.0 / (base ** (torch.arange(0, head_dim, 2, dtype=torch.float32) / head_dim))
-    positions = torch.arange(max_seq_len, dtype=torch.float32)
+    inv_freq = 1.0 / (base ** (torch.arange(0, head_dim, 2, dtype=torch.float32,
+                                            device="cpu") / head_dim))
+    positions = torch.arange(max_seq_len, dtype=torch.float32, device="cpu")
     freqs = torch.einsum("s,d->sd", positions, inv_freq)
     emb = torch.cat((freqs, freqs), dim=-1)
     cos, sin = emb.cos(), emb.sin()
@@ -48,7 +49,8 @@ def qk_norm_rope_decode(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
                         q_norm_weight: torch.Tensor, k_norm_weight: torch.Tensor, eps: float,
                         cos_table: torch.Tensor, sin_table: torch.Tensor, pool, layer_idx: int,
                         row_ids: torch.Tensor | None = None,
-                        out: torch.Tensor | None = None) -> torch.Tensor:
+                        out: torch.Tensor | None = None,
+                        positions: torch.Tensor | None = None) -> torch.Tensor:
     """Decode step of one layer: returns the normalised, rotated q
     (B, Hq, D) and writes normalised, rotated k and raw v into `pool`
     (a KVCachePool) at position seq_lens[row], the position RoPE uses too
@@ -57,6 +59,9 @@ def qk_norm_rope_decode(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
     q: (B, Hq, D), k/v: (B, Hkv, D) bf16 views, e.g. slices of the fused
     QKV projection output; row_ids: int32 (B,) rows of pool.block_table_2d
     (None: row b for token b).  Pages must already be reserved.
+    positions: int64 (B,) RoPE positions (the reference's position_ids);
+    None rotates at seq_lens[row], the write position, which is what the
+    reference's drivers pass.
     """
     _check_common(q, k, v, q_norm_weight, k_norm_weight, cos_table, sin_table)
     B, Hq, D = q.shape
@@ -69,6 +74,11 @@ def qk_norm_rope_decode(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
     if row_ids is not None:
         assert row_ids.dtype == torch.int32 and row_ids.numel() == B
         row_ids = row_ids.contiguous()
+    if positions is not None:
+        assert positions.dtype == torch.int64 and positions.numel() == B
+        positions = positions.reshape(-1)
+        if positions.stride(0) != 1:
+            positions = positions.contiguous()
     rc = _lib.load().qwen3_qk_norm_rope_decode_bf16(
         q.data_ptr(), _lib.strides(q, (0, 1)), k.data_ptr(), _lib.strides(k, (0, 1)),
         v.data_ptr(), _lib.strides(v, (0, 1)), q_norm_weight.data_ptr(),
@@ -77,7 +87,8 @@ def qk_norm_rope_decode(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
         out.data_ptr(), _lib.strides(out, (0, 1)),
         kb.data_ptr(), _lib.strides(kb, (0, 1, 2, 3)), vb.data_ptr(), _lib.strides(vb, (0, 1, 2, 3)),
         kb.shape[0], int(layer_idx), pool.seq_lens.data_ptr(), bt.data_ptr(), bt.stride(0),
-        bt.shape[0], bt.shape[1], _lib.ptr(row_ids), B, Hq, Hkv, D, kb.shape[3],
+        bt.shape[0], bt.shape[1], _lib.ptr(row_ids), _lib.ptr(positions), B, Hq, Hkv, D,
+        kb.shape[3],
         _lib.stream_of(dev))
     _lib.check(rc, "qwen3_qk_norm_rope_decode_bf16")
     return out

@@ -1,6 +1,6 @@
-"""The C-ABI library loads, exports every function include/qwen3_attn.h
-declares, and rejects bad arguments before launching anything.  CPU only: no
-call here reaches a kernel launch."""
+"""The C-ABI library loads, exports every function the headers under
+include/ declare, and rejects bad arguments before launching anything.  CPU
+only: no call here reaches a kernel launch."""
 import ctypes
 import re
 from pathlib import Path
@@ -10,18 +10,22 @@ import torch
 
 from qwen3_engine_from_scratch_amd import _lib
 
-HEADER = Path(__file__).resolve().parent.parent / "include" / "qwen3_attn.h"
+HEADERS = sorted((Path(__file__).resolve().parent.parent / "include").glob("*.h"))
 
 
 def declared_functions():
-    text = HEADER.read_text()
-    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
-    return sorted(set(re.findall(r"\b(qwen3_[a-z0-9_]+)\s*\(", text)))
+    names = set()
+    for h in HEADERS:
+        text = re.sub(r"/\*.*?\*/", "", h.read_text(), flags=re.S)
+        names |= set(re.findall(r"\b(qwen3_[a-z0-9_]+)\s*\(", text))
+    return sorted(names)
 
 
 def test_header_declares_the_abi():
     names = declared_functions()
+    assert [h.name for h in HEADERS] == ["qwen3_attn.h", "qwen3_model_ops.h"]
     assert "qwen3_paged_decode_bf16" in names and "qwen3_varlen_prefill_bf16" in names
+    assert "qwen3_argmax_bf16" in names
     assert sorted(names) == sorted(_lib.exported_symbols())
 
 
@@ -105,7 +109,7 @@ def test_pre_attention_rejects_bad_arguments():
         return lib.qwen3_qk_norm_rope_decode_bf16(
             q, q_strides, FAKE, ks, FAKE, ks, FAKE, FAKE, 1e-6, FAKE, FAKE, tab_stride, 64,
             FAKE, _s(2048, 128), FAKE, c4, FAKE, c4, 16, 0, FAKE, FAKE, bt_stride, 4, 8, None,
-            2, 16, 8, D, 16, None)
+            None, 2, 16, 8, D, 16, None)
 
     assert dec(D=64) == -3
     assert dec(q=None) == -1
@@ -121,6 +125,30 @@ def test_pre_attention_rejects_bad_arguments():
 
     assert slots(positions=None) == -1
     assert slots(D=256) == -3
+
+
+def test_model_ops_reject_bad_arguments():
+    lib = _lib.load()
+    # hidden not a multiple of 8 / too large; misaligned rows; null weight
+    assert lib.qwen3_add_rms_norm_bf16(None, 0, FAKE, 1024, None, 0, FAKE, 1e-6, FAKE, 1024,
+                                       None, 0, 4, 1020, None) == -3
+    assert lib.qwen3_add_rms_norm_bf16(None, 0, FAKE, 16384, None, 0, FAKE, 1e-6, FAKE, 16384,
+                                       None, 0, 4, 16384, None) == -3
+    assert lib.qwen3_add_rms_norm_bf16(FAKE, 1030, FAKE, 1024, None, 0, FAKE, 1e-6, FAKE, 1024,
+                                       None, 0, 4, 1024, None) == -2
+    assert lib.qwen3_add_rms_norm_bf16(None, 0, FAKE, 1024, None, 0, None, 1e-6, FAKE, 1024,
+                                       None, 0, 4, 1024, None) == -1
+    assert lib.qwen3_add_rms_norm_bf16(None, 0, FAKE, 1024, None, 0, FAKE, -1.0, FAKE, 1024,
+                                       None, 0, 4, 1024, None) == -1
+    assert lib.qwen3_silu_mul_bf16(FAKE, 6144, FAKE, 3072, 4, 3070, None) == -3
+    assert lib.qwen3_silu_mul_bf16(FAKE + 2, 6144, FAKE, 3072, 4, 3072, None) == -2
+    assert lib.qwen3_argmax_bf16(FAKE, 100, 4, 151936, FAKE, None) == -1  # row stride < vocab
+    assert lib.qwen3_argmax_bf16(None, 151936, 4, 151936, FAKE, None) == -1
+    assert lib.qwen3_advance_seq_lens(None, 8, FAKE, 4, -1, 1, None) == -1
+    # nothing to do: no launch, success
+    assert lib.qwen3_add_rms_norm_bf16(None, 0, FAKE, 1024, None, 0, FAKE, 1e-6, FAKE, 1024,
+                                       None, 0, 0, 1024, None) == 0
+    assert lib.qwen3_argmax_bf16(FAKE, 16, 0, 16, FAKE, None) == 0
 
 
 def test_kv_write_rejects_bad_arguments():

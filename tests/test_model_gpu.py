@@ -1,0 +1,281 @@
+"""Whole-model decode and prefill on the GPU: the row-wise kernels against
+their oracle formulas, the model against the fp32 oracle (itself pinned to
+the transformers Qwen3), the captured decode graphs against eager steps, and
+greedy generation through the batching engine.
+
+Bars:
+  add_rms_norm, silu_mul   within one bf16 ulp of the oracle, >= 99% of the
+                           values bit-identical (only fp32 summation order
+                           and exp rounding may differ); the residual stream
+                           and the embedding rows bit-exact.
+  argmax                   the index torch.argmax returns, exactly.
+  model logits             relative L2 error vs the fp32 oracle at most
+                           max(2 x that of the reference's own bf16 forward
+                           (the oracle's bf16 form), 0.03): the engine is no
+                           further from exact arithmetic than the reference.
+  graph replay             bit-identical to the eager step of the same
+                           batch, on every replay.
+  greedy tokens            each chosen token's fp32-oracle logit within
+                           0.15 of that step's maximum (a near-tie may go
+                           either way in bf16; a wrong token cannot).
+"""
+import pytest
+import torch
+
+from conftest import announce
+from oracle import inputs as oi
+from oracle import model as om
+
+pytestmark = pytest.mark.gpu
+
+
+def _ordered(t):
+    b = t.contiguous().view(torch.int16).to(torch.int32)
+    return torch.where(b >= 0, b, -(b & 0x7FFF))
+
+
+def assert_ulp_close(got, ref, what, max_ulps=1, min_exact=0.99):
+    d = (_ordered(got.cpu()) - _ordered(ref.cpu())).abs()
+    assert d.max().item() <= max_ulps, f"{what}: {d.max().item()} ulps"
+    exact = (d == 0).float().mean().item()
+    assert exact >= min_exact, f"{what}: only {exact:.4f} bit-identical"
+
+
+# ---- row-wise kernels --------------------------------------------------------
+
+@pytest.mark.parametrize("rows,hidden", [(1, 1024), (37, 1024), (64, 4096), (5, 5120), (3, 264)])
+def test_add_rms_norm_vs_oracle(gpu, rows, hidden):
+    from qwen3_engine_from_scratch_amd.kernels.model_ops import add_rms_norm
+
+    announce(f"add_rms_norm rows={rows} hidden={hidden}")
+    g = torch.Generator().manual_seed(rows + hidden)
+    x = (torch.randn(rows, hidden, generator=g) * 2).to(torch.bfloat16)
+    r = (torch.randn(rows, hidden, generator=g) * 3).to(torch.bfloat16)
+    w = (1 + 0.1 * torch.randn(hidden, generator=g)).to(torch.bfloat16)
+    h_ref = (r.float() + x.float()).to(torch.bfloat16)
+    n_ref = oi.rms_norm(h_ref, w, 1e-6)
+    rd = r.to(gpu)
+    out = add_rms_norm(x.to(gpu), rd, w.to(gpu), 1e-6, residual_out=rd)  # in place
+    torch.cuda.synchronize()
+    assert torch.equal(rd.cpu(), h_ref), "residual stream"
+    assert_ulp_close(out, n_ref, "normed")
+    # no add; strided rows
+    big = torch.zeros(rows, hidden + 64, dtype=torch.bfloat16)
+    big[:, :hidden] = r
+    out2 = add_rms_norm(None, big.to(gpu)[:, :hidden], w.to(gpu), 1e-6)
+    torch.cuda.synchronize()
+    assert_ulp_close(out2, oi.rms_norm(r, w, 1e-6), "normed (no add)")
+
+
+def test_embedding_and_row_selection(gpu):
+    from qwen3_engine_from_scratch_amd.kernels.model_ops import add_rms_norm, embed_rms_norm
+
+    announce("embed_rms_norm / row_index")
+    g = torch.Generator().manual_seed(7)
+    E = torch.randn(1000, 1024, generator=g).to(torch.bfloat16)
+    w = (1 + 0.1 * torch.randn(1024, generator=g)).to(torch.bfloat16)
+    ids = torch.tensor([5, 999, 0, 5, 1000, -3, 17], dtype=torch.int64)
+    hid, normed = embed_rms_norm(ids.to(gpu), E.to(gpu), w.to(gpu), 1e-6)
+    torch.cuda.synchronize()
+    ok = (ids >= 0) & (ids < 1000)
+    assert torch.equal(hid.cpu()[ok], E[ids[ok]])
+    assert not hid.cpu()[~ok].any() and not normed.cpu()[~ok].any(), "out-of-range ids -> zero rows"
+    assert_ulp_close(normed.cpu()[ok], oi.rms_norm(E[ids[ok]], w, 1e-6), "embedding norm")
+    # final-norm row selection
+    x = torch.randn(20, 1024, generator=g).to(torch.bfloat16)
+    sel = torch.tensor([19, 0, 7], dtype=torch.int64)
+    out = add_rms_norm(x.to(gpu), E[:20].to(gpu), w.to(gpu), 1e-6, row_index=sel.to(gpu))
+    torch.cuda.synchronize()
+    ref = oi.rms_norm((E[:20].float() + x.float()).to(torch.bfloat16)[sel], w, 1e-6)
+    assert_ulp_close(out, ref, "selected rows")
+
+
+@pytest.mark.parametrize("rows,inter", [(1, 3072), (64, 3072), (300, 8), (7, 12288)])
+def test_silu_mul_vs_torch(gpu, rows, inter):
+    from qwen3_engine_from_scratch_amd.kernels.model_ops import silu_mul
+
+    announce(f"silu_mul rows={rows} inter={inter}")
+    g = torch.Generator().manual_seed(rows * 7 + inter)
+    gu = (torch.randn(rows, 2 * inter, generator=g) * 4).to(torch.bfloat16)
+    ref = torch.nn.functional.silu(gu[:, :inter]) * gu[:, inter:]  # bf16 CPU, as qwen3/mlp.py:36
+    out = silu_mul(gu.to(gpu))
+    torch.cuda.synchronize()
+    assert_ulp_close(out, ref, "silu_mul")
+
+
+@pytest.mark.parametrize("rows,vocab", [(1, 151936), (64, 151936), (5, 1001), (3, 8)])
+def test_argmax_matches_torch(gpu, rows, vocab):
+    from qwen3_engine_from_scratch_amd.kernels.model_ops import argmax
+
+    announce(f"argmax rows={rows} vocab={vocab}")
+    g = torch.Generator().manual_seed(rows + vocab)
+    x = torch.randn(rows, vocab, generator=g).to(torch.bfloat16)
+    if rows >= 3:
+        x[0] = 0.5                                  # all tied: first index
+        x[1, vocab // 3] = x[1, -1] = 9.0           # tie between two maxima
+        x[2] = float("-inf")
+        x[2, vocab - 1] = -1e30
+    if rows >= 5:
+        x[3, vocab // 2] = float("nan")             # NaN ranks highest
+        x[4] = -0.0
+        x[4, 1] = 0.0                               # -0 == +0: first index
+    got = argmax(x.to(gpu)).cpu()
+    ref = torch.argmax(x, dim=-1)
+    assert torch.equal(got, ref), (got, ref)
+
+
+def test_advance_seq_lens(gpu):
+    from qwen3_engine_from_scratch_amd.kernels.model_ops import advance_seq_lens
+
+    announce("advance_seq_lens")
+    sl = torch.arange(10, dtype=torch.int32, device=gpu)
+    rows = torch.tensor([3, 9, 7, 7, 7, 0], dtype=torch.int32, device=gpu)
+    advance_seq_lens(sl, rows, skip_row=7)
+    torch.cuda.synchronize()
+    assert sl.cpu().tolist() == [1, 1, 2, 4, 4, 5, 6, 7, 8, 10]
+
+
+# ---- whole model -------------------------------------------------------------
+
+def _tiny(seed=0, layers=2, vocab=2048, hidden=512, inter=1024, hq=4, hkv=2):
+    from qwen3_engine_from_scratch_amd.config import Qwen3Config
+    from qwen3_engine_from_scratch_amd.model import Qwen3ForCausalLM, init_random_weights
+
+    cfg = Qwen3Config(hidden_size=hidden, num_attention_heads=hq, num_key_value_heads=hkv,
+                      head_dim=128, num_hidden_layers=layers, vocab_size=vocab,
+                      intermediate_size=inter, rms_norm_eps=1e-6, rope_theta=1e6,
+                      max_position_embeddings=1024, tie_word_embeddings=True)
+    m = init_random_weights(Qwen3ForCausalLM(cfg), seed=seed, std=0.05, norm_jitter=0.2)
+    m = m.to(torch.bfloat16)
+    state = {k: v.detach().float().clone() for k, v in m.state_dict().items()}
+    return m, state, cfg
+
+
+def _rel(a, b):
+    return ((a.float() - b.float()).norm() / b.float().norm()).item()
+
+
+def _pool(cfg, gpu, blocks=64, max_seq_len=512, max_requests=16):
+    from qwen3_engine_from_scratch_amd.PagedKVcache import KVCachePool
+
+    return KVCachePool(blocks, cfg.num_hidden_layers, 16, cfg.num_key_value_heads, cfg.head_dim,
+                       device=gpu, dtype=torch.bfloat16, max_seq_len=max_seq_len,
+                       max_requests=max_requests)
+
+
+def test_model_prefill_and_decode_vs_oracle(gpu):
+    """Drop-in forward: a padded prefill batch, then teacher-forced decode
+    steps; every position's logits against the fp32 oracle over the whole
+    sequence."""
+    from qwen3_engine_from_scratch_amd.PagedKVcache import PagedKVCache
+
+    model, state, cfg = _tiny(seed=1)
+    model = model.to(gpu)
+    lens = [37, 1, 90]
+    steps = 6
+    g = torch.Generator().manual_seed(3)
+    seqs = [torch.randint(0, cfg.vocab_size, (L + steps,), generator=g) for L in lens]
+    announce(f"model prefill lens={lens} + {steps} decode steps")
+    pool = _pool(cfg, gpu)
+    caches = [PagedKVCache(pool) for _ in lens]
+    S = max(lens)
+    padded = torch.zeros(len(lens), S, dtype=torch.long)
+    for i, L in enumerate(lens):
+        padded[i, :L] = seqs[i][:L]
+    out = [model(padded.to(gpu), kv_cache=caches, input_lens=lens).cpu()]
+    for s in range(steps):
+        ids = torch.stack([seqs[i][L + s] for i, L in enumerate(lens)])[:, None]
+        out.append(model(ids.to(gpu), kv_cache=caches).cpu())
+    torch.cuda.synchronize()
+    assert [c.seq_len for c in caches] == [L + steps for L in lens]
+    for i, L in enumerate(lens):
+        got = torch.cat([out[0][i, :L]] + [o[i] for o in out[1:]]).float()
+        ref = om.qwen3_logits_ref(state, cfg, seqs[i])
+        ref16 = om.qwen3_logits_ref(state, cfg, seqs[i], dtype=torch.bfloat16)
+        e, e16 = _rel(got, ref), _rel(ref16, ref)
+        announce(f"  request {i}: rel err {e:.4f} (reference bf16 forward: {e16:.4f})")
+        assert e <= max(2 * e16, 0.03), (i, e, e16)
+        assert out[0][i, L:].abs().sum() == 0, "pad positions are zero"
+
+
+def test_graph_runner_matches_eager_decode(gpu):
+    """The reference GraphRunner contract: replay(input_ids, positions, rows)
+    for k rows in a bucket of b equals the eager forward_decode of the same b
+    rows (dummy rows padding), bit for bit, on every replay."""
+    from qwen3_engine_from_scratch_amd.PagedKVcache import PagedKVCache
+    from qwen3_engine_from_scratch_amd.graph_runner import GraphRunner
+
+    model, state, cfg = _tiny(seed=2)
+    model = model.to(gpu)
+    pool = _pool(cfg, gpu, blocks=96, max_requests=24)
+    announce("graph runner: capture buckets 1,2,4,8")
+    runner = GraphRunner(model, pool, [PagedKVCache(pool) for _ in range(8)], (1, 2, 4, 8),
+                         reserve_pages=2)
+    # live requests with some context
+    g = torch.Generator().manual_seed(5)
+    reqs = [PagedKVCache(pool) for _ in range(5)]
+    for i, c in enumerate(reqs):
+        L = 10 + 7 * i
+        model(torch.randint(0, cfg.vocab_size, (1, L), generator=g).to(gpu), kv_cache=c)
+    k_buf, v_buf = pool.k_buffer.clone(), pool.v_buffer.clone()
+    for k in (5, 3, 1, 5):
+        b = runner.bucket_for(k)
+        act = reqs[:k]
+        for c in act:
+            c.reserve_next()
+        ids = torch.randint(0, cfg.vocab_size, (k, 1), generator=g).to(gpu)
+        pos = torch.tensor([[c.seq_len] for c in act], dtype=torch.long).to(gpu)
+        rows = torch.tensor([c.row_id for c in act], dtype=torch.int32).to(gpu)
+        announce(f"  replay k={k} bucket={b}")
+        got = runner.replay(ids, pos, rows)[:k].clone()
+        # eager on the same padded batch, from the same pool contents
+        pool.k_buffer.copy_(k_buf)
+        pool.v_buffer.copy_(v_buf)
+        pad = torch.full((b,), runner.dummy_row, dtype=torch.int32, device=gpu)
+        pad[:k] = rows
+        pids = torch.zeros(b, 1, dtype=torch.long, device=gpu)
+        pids[:k] = ids
+        ppos = runner.graphs[b][1]["pos"].clone()
+        ref = model.forward_decode(pids, ppos, pad, [reqs[0]] * b)[:k]
+        torch.cuda.synchronize()
+        assert torch.equal(got, ref), f"k={k}: replay differs from eager"
+        for _ in range(2):  # replays after eager work give the same result
+            again = runner.replay(ids, pos, rows)[:k]
+            torch.cuda.synchronize()
+            assert torch.equal(again, got)
+        k_buf, v_buf = pool.k_buffer.clone(), pool.v_buffer.clone()
+    runner.free()
+
+
+def test_engine_greedy_generation_vs_oracle(gpu):
+    """Continuous batching with captured decode graphs (greedy argmax and
+    length advance inside the graph): every generated token is the fp32
+    oracle's choice up to bf16 near-ties, and the eager engine agrees."""
+    from qwen3_engine_from_scratch_amd.engine import Engine, GenRequest
+
+    model, state, cfg = _tiny(seed=4)
+    model = model.to(gpu)
+    g = torch.Generator().manual_seed(11)
+    lens = [5, 63, 17, 40, 1, 33]
+    new = [12, 3, 20, 7, 9, 1]
+    prompts = [torch.randint(0, cfg.vocab_size, (L,), generator=g).tolist() for L in lens]
+    results = {}
+    for use_graph in (True, False):
+        pool = _pool(cfg, gpu, blocks=128, max_requests=32)
+        announce(f"engine use_graph={use_graph}, max_batch=4, {len(lens)} requests")
+        eng = Engine(model, pool, max_batch=4, use_graph=use_graph)
+        reqs = [GenRequest(i, p, n) for i, (p, n) in enumerate(zip(prompts, new))]
+        stats = eng.generate(reqs)
+        eng.close()
+        assert stats["output_tokens"] == sum(new)
+        assert [len(r.output_ids) for r in reqs] == new
+        assert pool.free_count == pool.total_blocks, "pages not returned"
+        results[use_graph] = [r.output_ids for r in reqs]
+    for i, (p, out) in enumerate(zip(prompts, results[True])):
+        ref = om.qwen3_logits_ref(state, cfg, torch.tensor(p + out[:-1]))
+        steps = ref[len(p) - 1:]
+        chosen = steps[torch.arange(len(out)), torch.tensor(out)]
+        gap = (steps.max(-1).values - chosen).max().item()
+        assert gap <= 0.15, (i, gap)
+    agree = sum(a == b for x, y in zip(results[True], results[False]) for a, b in zip(x, y))
+    assert agree >= 0.9 * sum(new), "graph and eager engines disagree beyond near-ties"

@@ -374,3 +374,89 @@ def test_qk_norm_rope_ref_composes_the_two_steps():
     q, k = opa.qk_norm_rope_ref(x, kx, w, kw, 1e-6, cos, sin, pos)
     assert torch.equal(q, oi.apply_rope(oi.rms_norm(x, w, 1e-6), cos[pos], sin[pos]))
     assert _rope_err(k, oi.rms_norm(kx, kw, 1e-6), pos) < 2.0 ** -6
+
+
+# ---- whole-model forward ---------------------------------------------------
+
+from oracle import model as om  # noqa: E402
+
+
+def _tiny_hf_model(seed=0, layers=2, vocab=512, hidden=256, inter=384, hq=4, hkv=2, tie=True):
+    """A random-weight transformers Qwen3 (an independent implementation of
+    the architecture) and the same weights under the reference's fused names."""
+    from transformers import Qwen3Config as HFConfig, Qwen3ForCausalLM as HFModel
+
+    from qwen3_engine_from_scratch_amd.config import Qwen3Config
+
+    hc = HFConfig(vocab_size=vocab, hidden_size=hidden, intermediate_size=inter,
+                  num_hidden_layers=layers, num_attention_heads=hq, num_key_value_heads=hkv,
+                  head_dim=128, rms_norm_eps=1e-6, rope_theta=1e6, tie_word_embeddings=tie,
+                  max_position_embeddings=512, attention_bias=False)
+    hc._attn_implementation = "eager"
+    torch.manual_seed(seed)
+    hf = HFModel(hc).float().eval()
+    with torch.no_grad():
+        for name, p in hf.named_parameters():
+            if name.endswith("norm.weight"):
+                p.copy_(1 + 0.2 * torch.randn_like(p))
+            else:
+                p.copy_(0.05 * torch.randn_like(p))
+    sd = hf.state_dict()
+    state = {}
+    for name, t in sd.items():
+        if ".q_proj." in name:
+            base = name.replace(".q_proj.", ".qkv_proj.")
+            state[base] = torch.cat([t, sd[name.replace(".q_proj.", ".k_proj.")],
+                                     sd[name.replace(".q_proj.", ".v_proj.")]])
+        elif ".gate_proj." in name:
+            state[name.replace(".gate_proj.", ".gate_up_proj.")] = torch.cat(
+                [t, sd[name.replace(".gate_proj.", ".up_proj.")]])
+        elif not any(s in name for s in (".k_proj.", ".v_proj.", ".up_proj.")):
+            state[name] = t
+    if tie:
+        state.pop("lm_head.weight", None)
+    cfg = Qwen3Config(hidden_size=hidden, num_attention_heads=hq, num_key_value_heads=hkv,
+                      head_dim=128, num_hidden_layers=layers, vocab_size=vocab,
+                      intermediate_size=inter, rms_norm_eps=1e-6, rope_theta=1e6,
+                      max_position_embeddings=512, tie_word_embeddings=tie)
+    return hf, state, cfg
+
+
+def _hf_logits(hf, ids):
+    with torch.no_grad():
+        return hf(torch.as_tensor(ids)[None]).logits[0].float()
+
+
+@pytest.mark.parametrize("tie,hq,hkv", [(True, 4, 2), (False, 4, 4), (True, 8, 2)])
+def test_model_oracle_matches_transformers_qwen3(tie, hq, hkv):
+    hf, state, cfg = _tiny_hf_model(seed=hq + hkv, tie=tie, hq=hq, hkv=hkv)
+    ids = torch.randint(0, cfg.vocab_size, (45,), generator=torch.Generator().manual_seed(1))
+    ref = _hf_logits(hf, ids)
+    got = om.qwen3_logits_ref(state, cfg, ids)
+    assert (got - ref).abs().max().item() < 2e-4 * ref.abs().max().item()
+    # the bf16 form of the same steps stays within bf16 rounding of fp32
+    b16 = om.qwen3_logits_ref(state, cfg, ids, dtype=torch.bfloat16)
+    rel = ((b16 - ref).norm() / ref.norm()).item()
+    assert 1e-4 < rel < 5e-2
+
+
+def test_model_oracle_rejects_planted_mistakes(monkeypatch):
+    hf, state, cfg = _tiny_hf_model(seed=3, hq=4, hkv=2)
+    ids = torch.randint(0, cfg.vocab_size, (40,), generator=torch.Generator().manual_seed(2))
+    ref = _hf_logits(hf, ids)
+
+    def err():
+        got = om.qwen3_logits_ref(state, cfg, ids)
+        return (got - ref).abs().max().item() / ref.abs().max().item()
+
+    assert err() < 2e-4
+    planted = {
+        "_rotate_half": lambda x: torch.stack((-x[..., 1::2], x[..., ::2]), -1).flatten(-2),
+        "_expand_kv": lambda x, G: x.repeat(G, 1, 1),                 # h % Hkv head map
+        "_rms": lambda x, w, eps: (x.float() * torch.rsqrt(
+            x.float().pow(2).mean(-1, keepdim=True) + eps)).to(x.dtype),  # weight dropped
+    }
+    for name, fn in planted.items():
+        with monkeypatch.context() as m:
+            m.setattr(om, name, fn)
+            assert err() > 1e-2, name
