@@ -13,6 +13,16 @@
  *                              (qwen3/mlp.py:31-36)
  *   qwen3_argmax_bf16       <- the greedy path of sample_tokens
  *                              (qwen3/sampling.py:256-258: logits.argmax(-1))
+ *   qwen3_decode_linear_bf16 <- the nn.Linear projections of a decode step
+ *                              (qkv_proj qwen3/attention.py:81, o_proj :187,
+ *                              gate_up_proj / down_proj qwen3/mlp.py:34-36,
+ *                              lm_head qwen3/model.py:241) for batches of at
+ *                              most 64 rows, with the RMSNorm before them, the
+ *                              residual add after them or the SwiGLU activation
+ *                              between them folded in
+ *   qwen3_embed_ss_bf16     <- the embedding lookup (qwen3/model.py:212) writing
+ *                              the residual stream and its partial sums of squares
+ *                              for the fused first norm
  *   qwen3_advance_seq_lens  <- the resident-length write of
  *                              PagedKVCache.advance_seq_len
  *                              (qwen3/PagedKVcache.py:216-219), one launch for
@@ -58,6 +68,38 @@ int qwen3_silu_mul_bf16(const void* gate_up, int64_t gate_up_row_stride,
  * every number (torch.argmax's rule). */
 int qwen3_argmax_bf16(const void* logits, int64_t row_stride, int64_t rows,
                       int64_t vocab, int64_t* out, void* stream);
+
+/* Decode-batch linear layer y = a @ W^T for M <= 64 rows; W (weight) is
+ * nn.Linear's (out x in) row-major matrix, K its input width (a multiple of
+ * 128), N the output columns (a multiple of 16).
+ * Prologue: with ss_in NULL, a = x.  Otherwise x is the residual stream h and
+ *   a = bf16((h * rsqrt(mean(h^2) + eps)) * norm_weight), with sum(h^2) of
+ *   row r taken as the sum of ss_in[r * ss_in_tiles + t] over t (partial sums
+ *   written by the kernel that produced h).
+ * Epilogue (epilogue argument):
+ *   0 store     y[r, n] = bf16(acc)
+ *   1 residual  h' = bf16(residual[r, n] + bf16(acc)) into residual_out, and
+ *               ss_out[r * (N / 16) + n / 16] = sum of h'^2 over those 16 columns
+ *               (residual_out must not alias residual)
+ *   2 silu      gate rows are weight rows [0, N), up rows [up_row, up_row + N):
+ *               y[r, n] = bf16(bf16(silu(bf16(gate))) * bf16(up))
+ * Results do not depend on timing (fixed summation order). */
+int qwen3_decode_linear_bf16(const void* x, int64_t x_row_stride,
+                             const float* ss_in, int ss_in_tiles,
+                             const void* norm_weight, float eps,
+                             const void* weight, int64_t weight_row_stride,
+                             int M, int N, int K, int epilogue,
+                             void* y, int64_t y_row_stride,
+                             const void* residual, int64_t residual_row_stride,
+                             void* residual_out, int64_t residual_out_row_stride,
+                             float* ss_out, int up_row, void* stream);
+
+/* h_out[r] = embedding[ids[r]] (zero row for an id outside [0, vocab)) and
+ * ss_out[r * (hidden / 16) + t] = sum of h^2 over columns 16t .. 16t + 15:
+ * the input of the first decode_linear with a norm prologue. */
+int qwen3_embed_ss_bf16(const int64_t* ids, const void* embedding,
+                        int64_t embedding_row_stride, int64_t vocab, int hidden, int M,
+                        void* h_out, int64_t h_row_stride, float* ss_out, void* stream);
 
 /* seq_lens[row_ids[i]] += delta for i < n, except rows equal to skip_row
  * (a captured batch's padding row) and rows outside [0, max_rows).  Rows

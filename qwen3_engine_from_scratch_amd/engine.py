@@ -17,7 +17,11 @@ the per-step state lives:
     rows once;
   - pages for the next token are reserved for the whole batch with one pool
     allocation and one block-table write (reserve_pages_bulk);
-  - the host reads back only the B new token ids per step.
+  - the host reads back only the B new token ids per step, and does so
+    after it has launched the next step (whose inputs are already on the
+    device), so its bookkeeping overlaps the GPU.  A request's count limit
+    is known without the read-back; an eos seen one step late drops the one
+    token computed past it (its page writes land beyond its final length).
 Greedy decoding only (temperature 0), as the reference's benchmark runs.
 """
 from __future__ import annotations
@@ -47,11 +51,18 @@ class GenRequest:
     cache: PagedKVCache | None = None
     finished: bool = False
     finish_time: float = 0.0
+    inflight: int = 0        # decode steps launched whose token has not been read back
+    eos_hit: bool = False
 
     def is_finished(self) -> bool:
-        return (len(self.output_ids) >= self.max_new_tokens
-                or (self.eos_token_id is not None and bool(self.output_ids)
-                    and self.output_ids[-1] == self.eos_token_id))
+        """Reference rule (qwen3/request.py:121-137): max_new_tokens reached
+        or the last token is eos."""
+        return len(self.output_ids) >= self.max_new_tokens or self.eos_hit
+
+    def schedulable(self) -> bool:
+        """May take part in another decode step: counts the steps in flight,
+        so the count limit needs no read-back."""
+        return not self.eos_hit and len(self.output_ids) + self.inflight < self.max_new_tokens
 
 
 class Engine:
@@ -69,8 +80,13 @@ class Engine:
                                       greedy=True, advance=True, positions_from_lengths=True)
         else:
             model.reserve_decode_workspace(max_batch, pool)
-        self._tok_host = torch.empty(max(max_batch, 1), dtype=torch.int64, pin_memory=True)
-        self._last_batch = None  # (bucket, tuple of request ids) of the last graph replay
+        # two pinned landing buffers: a step's tokens are read back while the
+        # next step's copy is already queued
+        self._tok_host = [torch.empty(max(max_batch, 1), dtype=torch.int64, pin_memory=True)
+                          for _ in range(2)]
+        self._flip = 0
+        self._pending = None     # (requests, host view, event) of the last decode launch
+        self._last_batch = None  # (bucket, request ids) of the last graph replay
 
     # ---- steps -------------------------------------------------------------
 
@@ -103,18 +119,45 @@ class Engine:
         toks = argmax(logits).cpu().tolist()
         for r, L, tok in zip(reqs, lens, toks):
             r.cache.seq_len = L
-            r.output_ids.append(int(tok))
+            self._take(r, int(tok))
         set_seq_lens_bulk([r.cache for r in reqs])
 
+    @staticmethod
+    def _take(r, tok: int) -> None:
+        if r.eos_hit or len(r.output_ids) >= r.max_new_tokens:
+            return  # a step launched before the stop was known: its token is dropped
+        r.output_ids.append(tok)
+        if r.eos_token_id is not None and tok == r.eos_token_id:
+            r.eos_hit = True
+
+    def _drain(self) -> None:
+        """Reads back the tokens of the decode step in flight."""
+        if self._pending is None:
+            return
+        reqs, host, ev = self._pending
+        self._pending = None
+        ev.synchronize()
+        for r, tok in zip(reqs, host.tolist()):
+            r.inflight -= 1
+            self._take(r, int(tok))
+
     def _decode(self, reqs) -> None:
+        """Launches one decode step for `reqs` and then reads back the tokens
+        of the step before it, so the host's bookkeeping overlaps the GPU."""
         k = len(reqs)
-        caches = [r.cache for r in reqs]
-        # the token of this step lands at position seq_len: reserve its page
-        reserve_pages_bulk(caches, [c.seq_len + 1 for c in caches])
         dev = self.device
         if self.runner is not None:
             b = self.runner.bucket_for(k)
             key = (b, tuple(r.request_id for r in reqs))
+            if key != self._last_batch:
+                # a changed batch takes its input tokens from the host
+                self._drain()
+        else:
+            self._drain()
+        caches = [r.cache for r in reqs]
+        # the token of this step lands at position seq_len: reserve its page
+        reserve_pages_bulk(caches, [c.seq_len + 1 for c in caches])
+        if self.runner is not None:
             if key == self._last_batch:
                 out = self.runner.replay_greedy(k)
             else:
@@ -128,45 +171,53 @@ class Engine:
             rows = torch.tensor([c.row_id for c in caches], dtype=torch.int32).to(dev)
             logits = self.model.decode_logits(ids, rows, self.pool)
             toks = argmax(logits)
-        host = self._tok_host[:k]
+        host = self._tok_host[self._flip][:k]
+        self._flip ^= 1
         host.copy_(toks, non_blocking=True)
-        torch.cuda.current_stream(dev).synchronize()
+        ev = torch.cuda.Event()
+        ev.record(torch.cuda.current_stream(dev))
+        for r in reqs:
+            r.inflight += 1
         for c in caches:
             c.seq_len += 1
         if self.runner is None:
             set_seq_lens_bulk(caches)
-        for r, tok in zip(reqs, host.tolist()):
-            r.output_ids.append(int(tok))
+        self._drain()
+        self._pending = (list(reqs), host, ev)
 
     # ---- loop --------------------------------------------------------------
 
     @torch.no_grad()
     def generate(self, requests: list) -> dict:
-        """Runs every request to completion; returns timing and counts."""
+        """Runs every request to completion; returns timing and counts.
+        Timing: prefill_s / decode_s are host wall time per kind of step
+        (a decode step's read-back overlaps the next launch)."""
         waiting = deque(requests)
         running: list = []
+        self._pending = None
+        self._last_batch = None
         t0 = time.perf_counter()
         prefill_s = decode_s = 0.0
         n_prefill = n_decode = 0
         while waiting or running:
             ts = time.perf_counter()
             if waiting and len(running) < self.max_batch:
+                self._drain()
                 take = [waiting.popleft()
                         for _ in range(min(self.max_batch - len(running), len(waiting)))]
                 self._prefill(take)
                 running.extend(take)
-                batch, is_prefill = take, True
-            else:
-                batch, is_prefill = running[:self.max_batch], False
-                self._decode(batch)
-            dt = time.perf_counter() - ts
-            if is_prefill:
-                prefill_s += dt
+                prefill_s += time.perf_counter() - ts
                 n_prefill += 1
             else:
-                decode_s += dt
-                n_decode += 1
-            done = [r for r in batch if r.is_finished()]
+                batch = [r for r in running if r.schedulable()][:self.max_batch]
+                if batch:
+                    self._decode(batch)
+                    n_decode += 1
+                else:
+                    self._drain()
+                decode_s += time.perf_counter() - ts
+            done = [r for r in running if r.inflight == 0 and r.is_finished()]
             if done:
                 now = time.perf_counter() - t0
                 for r in done:
@@ -175,6 +226,7 @@ class Engine:
                     r.cache.free()
                     r.cache = None
                 running = [r for r in running if not r.finished]
+        self._drain()
         total = time.perf_counter() - t0
         n_tok = sum(len(r.output_ids) for r in requests)
         return {"total_s": total, "output_tokens": n_tok, "tokens_per_s": n_tok / total,
@@ -182,6 +234,7 @@ class Engine:
                 "decode_steps": n_decode}
 
     def close(self):
+        self._drain()
         if self.runner is not None:
             self.runner.free()
         for c in self._placeholders:

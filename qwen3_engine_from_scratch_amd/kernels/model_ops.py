@@ -1,10 +1,12 @@
-"""Row-wise kernels around the attention path of a Qwen3 decoder step, on
-the gfx950 HIP library (include/qwen3_model_ops.h): residual add + RMSNorm
-(also the embedding lookup and the final-norm row selection), SwiGLU
-activation, greedy token choice and the resident-length advance.
+"""Kernels around the attention path of a Qwen3 decoder step, on the gfx950
+HIP library (include/qwen3_model_ops.h): residual add + RMSNorm (also the
+embedding lookup and the final-norm row selection), SwiGLU activation,
+greedy token choice, the resident-length advance, and the decode-batch
+linear layers with the norm / residual add / activation folded in.
 
 Reference modules: qwen3/norm.py:22-26, qwen3/decoder.py:49,55,
-qwen3/mlp.py:31-36, qwen3/sampling.py:256-258, qwen3/PagedKVcache.py:216-219.
+qwen3/mlp.py:31-36, qwen3/attention.py:81,187, qwen3/model.py:212,241,
+qwen3/sampling.py:256-258, qwen3/PagedKVcache.py:216-219.
 """
 from __future__ import annotations
 
@@ -12,7 +14,11 @@ import torch
 
 from .. import _lib
 
-__all__ = ["add_rms_norm", "embed_rms_norm", "silu_mul", "argmax", "advance_seq_lens"]
+__all__ = ["add_rms_norm", "embed_rms_norm", "silu_mul", "argmax", "advance_seq_lens",
+           "decode_linear", "embed_ss", "DECODE_LINEAR_MAX_ROWS"]
+
+DECODE_LINEAR_MAX_ROWS = 64
+_EPI = {"store": 0, "residual": 1, "silu": 2}
 
 
 def _rows2d(t: torch.Tensor) -> torch.Tensor:
@@ -122,3 +128,65 @@ def advance_seq_lens(seq_lens: torch.Tensor, row_ids: torch.Tensor, skip_row: in
                                             row_ids.data_ptr(), row_ids.numel(), int(skip_row),
                                             int(delta), _lib.stream_of(dev))
     _lib.check(rc, "qwen3_advance_seq_lens")
+
+
+def decode_linear(x: torch.Tensor, weight: torch.Tensor, *, epilogue: str = "store",
+                  ss_in: torch.Tensor | None = None, norm_weight: torch.Tensor | None = None,
+                  eps: float = 1e-6, residual: torch.Tensor | None = None,
+                  residual_out: torch.Tensor | None = None, ss_out: torch.Tensor | None = None,
+                  out: torch.Tensor | None = None) -> torch.Tensor | None:
+    """y = a @ weight^T for at most 64 rows (a decode batch), weight the
+    (out, in) nn.Linear matrix.  With ss_in (rows, tiles) fp32 partial sums
+    of x^2 and norm_weight, a = RMSNorm(x) computed on the fly.  Epilogues:
+      "store"     returns y (rows, out) bf16;
+      "residual"  residual_out = bf16(residual + bf16(y)) and ss_out
+                  (rows, out/16) its per-16-column sums of squares; returns None;
+      "silu"      weight holds gate then up rows (2I, in): returns
+                  bf16(bf16(silu(gate)) * up), (rows, I).
+    """
+    x = _rows2d(x)
+    M, K = x.shape
+    assert weight.dim() == 2 and weight.stride(1) == 1 and weight.shape[1] == K
+    assert x.dtype == weight.dtype == torch.bfloat16
+    epi = _EPI[epilogue]
+    N = weight.shape[0] // 2 if epilogue == "silu" else weight.shape[0]
+    if ss_in is not None:
+        assert ss_in.dtype == torch.float32 and ss_in.is_contiguous() and ss_in.shape[0] == M
+        assert norm_weight is not None and norm_weight.is_contiguous() and norm_weight.numel() == K
+    if epilogue == "residual":
+        assert residual is not None and residual_out is not None and ss_out is not None
+        assert residual.shape == residual_out.shape == (M, N)
+        assert ss_out.dtype == torch.float32 and ss_out.is_contiguous() and ss_out.shape == (M, N // 16)
+        assert residual_out.data_ptr() != residual.data_ptr(), "residual_out must not alias residual"
+    elif out is None:
+        out = torch.empty(M, N, dtype=x.dtype, device=x.device)
+    dev = _lib.require_hip(x, weight, ss_in, norm_weight, residual, residual_out, ss_out, out)
+    rc = _lib.load().qwen3_decode_linear_bf16(
+        x.data_ptr(), x.stride(0), _lib.ptr(ss_in), ss_in.shape[1] if ss_in is not None else 0,
+        _lib.ptr(norm_weight), float(eps), weight.data_ptr(), weight.stride(0), M, N, K, epi,
+        _lib.ptr(out), out.stride(0) if out is not None else 0,
+        _lib.ptr(residual), residual.stride(0) if residual is not None else 0,
+        _lib.ptr(residual_out), residual_out.stride(0) if residual_out is not None else 0,
+        _lib.ptr(ss_out), N if epilogue == "silu" else 0, _lib.stream_of(dev))
+    _lib.check(rc, "qwen3_decode_linear_bf16")
+    return out if epilogue != "residual" else None
+
+
+def embed_ss(ids: torch.Tensor, embed_weight: torch.Tensor, *, h_out: torch.Tensor | None = None,
+             ss_out: torch.Tensor | None = None) -> tuple[torch.Tensor, torch.Tensor]:
+    """Embedding rows (tokens, hidden) bf16 plus their per-16-column sums of
+    squares (tokens, hidden/16) fp32, the input of a normed decode_linear."""
+    ids = ids.reshape(-1)
+    assert ids.dtype == torch.int64 and ids.is_contiguous()
+    V, H = embed_weight.shape
+    M = ids.numel()
+    if h_out is None:
+        h_out = torch.empty(M, H, dtype=embed_weight.dtype, device=embed_weight.device)
+    if ss_out is None:
+        ss_out = torch.empty(M, H // 16, dtype=torch.float32, device=embed_weight.device)
+    dev = _lib.require_hip(ids, embed_weight, h_out, ss_out)
+    rc = _lib.load().qwen3_embed_ss_bf16(ids.data_ptr(), embed_weight.data_ptr(),
+                                         embed_weight.stride(0), V, H, M, h_out.data_ptr(),
+                                         h_out.stride(0), ss_out.data_ptr(), _lib.stream_of(dev))
+    _lib.check(rc, "qwen3_embed_ss_bf16")
+    return h_out, ss_out

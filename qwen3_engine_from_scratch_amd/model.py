@@ -33,7 +33,8 @@ import torch.nn.functional as F
 
 from .config import Qwen3Config
 from .kernels.flash_attention_varlen import flash_attention_prefill
-from .kernels.model_ops import add_rms_norm, embed_rms_norm, silu_mul
+from .kernels.model_ops import (DECODE_LINEAR_MAX_ROWS, add_rms_norm, decode_linear,
+                                embed_rms_norm, embed_ss, silu_mul)
 from .kernels.paged_attention import paged_attention_decode_hip, paged_decode_workspace_bytes
 from .kernels.pre_attention import qk_norm_rope_decode, qk_norm_rope_prefill, rope_tables
 
@@ -170,15 +171,54 @@ class Qwen3ForCausalLM(nn.Module):
             self._workspace = torch.empty(max(need, 1), dtype=torch.uint8,
                                           device=pool.k_buffer.device)
 
+    def fused_decode_ok(self, batch: int) -> bool:
+        """Whether a decode step of `batch` rows runs on the fused decode
+        linears (at most 64 rows; widths the kernels tile)."""
+        c = self.config
+        widths = (c.hidden_size, c.num_attention_heads * c.head_dim, c.intermediate_size)
+        return (batch <= DECODE_LINEAR_MAX_ROWS and all(w % 128 == 0 for w in widths)
+                and c.vocab_size % 16 == 0)
+
+    def _decode_fused(self, ids, attend) -> torch.Tensor:
+        """Decode step on the fused linears: the residual stream ping-pongs
+        between two buffers, each with its per-16-column sums of squares, so
+        every RMSNorm is the prologue of the linear after it and every
+        residual add the epilogue of the linear before it."""
+        cfg = self.config
+        eps = cfg.rms_norm_eps
+        layers = self.model.layers
+        B = ids.numel()
+        H, I = cfg.hidden_size, cfg.intermediate_size
+        h_a, ss_a = embed_ss(ids, self.model.embed_tokens.weight)
+        h_b = torch.empty_like(h_a)
+        ss_b = torch.empty_like(ss_a)
+        for i, layer in enumerate(layers):
+            at = layer.self_attn
+            qkv = decode_linear(h_a, at.qkv_proj.weight, ss_in=ss_a,
+                                norm_weight=layer.input_layernorm.weight, eps=eps)
+            decode_linear(attend(i, at, qkv), at.o_proj.weight, epilogue="residual",
+                          residual=h_a, residual_out=h_b, ss_out=ss_b)
+            act = decode_linear(h_b, layer.mlp.gate_up_proj.weight, epilogue="silu", ss_in=ss_b,
+                                norm_weight=layer.post_attention_layernorm.weight, eps=eps)
+            decode_linear(act, layer.mlp.down_proj.weight, epilogue="residual",
+                          residual=h_b, residual_out=h_a, ss_out=ss_a)
+        # lm_head streams 311 MB of weights for few rows: the library GEMM
+        # after a separate final norm
+        final = add_rms_norm(None, h_a, self.model.norm.weight, eps)
+        return F.linear(final, self.lm_head.weight)
+
     @torch.no_grad()
     def decode_logits(self, ids: torch.Tensor, row_ids: torch.Tensor, pool,
-                      positions: torch.Tensor | None = None) -> torch.Tensor:
+                      positions: torch.Tensor | None = None,
+                      fused: bool | None = None) -> torch.Tensor:
         """One decode step for B requests: ids (B,) int64 (this step's input
         tokens), row_ids (B,) int32 resident-table rows.  Writes each token's
         K/V at position seq_lens[row] (pages must be reserved), attends over
         seq_lens[row] + 1 tokens and returns logits (B, V).  positions
         (B,) int64: RoPE positions (None: seq_lens[row]).  Does not advance
-        seq_lens (the caller's job, as in the reference)."""
+        seq_lens (the caller's job, as in the reference).  fused (None: when
+        possible) selects the fused decode linears over the library GEMMs
+        with separate norm / activation kernels."""
         B = ids.numel()
         cfg = self.config
         cos, sin = self.model.rotary_emb.tables(ids.device)
@@ -193,9 +233,13 @@ class Qwen3ForCausalLM(nn.Module):
                                      positions=positions)
             o = paged_attention_decode_hip(qr, pool.k_buffer[:, i], pool.v_buffer[:, i],
                                            pool.block_table_2d, pool.seq_lens, row_ids,
-                                           pool.block_size, workspace=ws)
+                                           pool.block_size)
             return o.view(B, Hq * D)
 
+        if fused is None:
+            fused = self.fused_decode_ok(B)
+        if fused:
+            return self._decode_fused(ids.reshape(-1).contiguous(), attend)
         return self._run(ids.reshape(-1), attend, None)
 
     @torch.no_grad()

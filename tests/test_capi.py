@@ -145,6 +145,16 @@ def test_model_ops_reject_bad_arguments():
     assert lib.qwen3_argmax_bf16(FAKE, 100, 4, 151936, FAKE, None) == -1  # row stride < vocab
     assert lib.qwen3_argmax_bf16(None, 151936, 4, 151936, FAKE, None) == -1
     assert lib.qwen3_advance_seq_lens(None, 8, FAKE, 4, -1, 1, None) == -1
+    def lin(M=64, N=1024, K=2048, epi=0, y=FAKE, ss_in=None, nw=FAKE):
+        return lib.qwen3_decode_linear_bf16(FAKE, K, ss_in, 64, nw, 1e-6, FAKE, K, M, N, K, epi,
+                                            y, N, FAKE, N, FAKE + 4096, N, FAKE, 0, None)
+
+    assert lin(M=65) == -1                 # more rows than a decode batch
+    assert lin(N=1000) == -3 and lin(K=1000) == -3
+    assert lin(epi=3) == -1
+    assert lin(y=None) == -1
+    assert lin(ss_in=FAKE, nw=None) == -1  # norm prologue without its weight
+    assert lin(epi=2, N=1024) == -1        # silu: up half must start at or after row N
     # nothing to do: no launch, success
     assert lib.qwen3_add_rms_norm_bf16(None, 0, FAKE, 1024, None, 0, FAKE, 1e-6, FAKE, 1024,
                                        None, 0, 0, 1024, None) == 0

@@ -8,6 +8,10 @@ Bars:
                            values bit-identical (only fp32 summation order
                            and exp rounding may differ); the residual stream
                            and the embedding rows bit-exact.
+  decode_linear            |got - ref| <= 2^-7 |ref| + 2^-9 max|ref| of the row
+                           against the fp32 product rounded to bf16 (outputs
+                           that nearly cancel move by more than an ulp when
+                           the fp32 summation order changes).
   argmax                   the index torch.argmax returns, exactly.
   model logits             relative L2 error vs the fp32 oracle at most
                            max(2 x that of the reference's own bf16 forward
@@ -135,6 +139,82 @@ def test_advance_seq_lens(gpu):
     assert sl.cpu().tolist() == [1, 1, 2, 4, 4, 5, 6, 7, 8, 10]
 
 
+def _close(got, ref, what):
+    """|got - ref| <= 2^-7 |ref| + 2^-9 max|ref| per row: one bf16 ulp of the
+    output (a rounding that tips the other way) plus what a different fp32
+    summation order, or a one-ulp change of a normalised input entry, moves an
+    output that nearly cancels."""
+    got, ref = got.float().cpu(), ref.float().cpu()
+    bound = ref.abs() * 2 ** -7 + ref.abs().amax(-1, keepdim=True) * 2 ** -9
+    bad = (got - ref).abs() > bound
+    assert not bad.any(), f"{what}: {int(bad.sum())} values off, max {(got - ref).abs().max():.3g}"
+
+
+@pytest.mark.parametrize("M,K,N", [(1, 1024, 4096), (64, 1024, 4096), (37, 2048, 1024),
+                                   (64, 3072, 1024), (5, 128, 16)])
+def test_decode_linear_store_and_norm(gpu, M, K, N):
+    from qwen3_engine_from_scratch_amd.kernels.model_ops import decode_linear
+
+    announce(f"decode_linear M={M} K={K} N={N}")
+    g = torch.Generator().manual_seed(M * 31 + K + N)
+    x = torch.randn(M, K, generator=g).to(torch.bfloat16)
+    W = (torch.randn(N, K, generator=g) * 0.05).to(torch.bfloat16)
+    wn = (1 + 0.1 * torch.randn(K, generator=g)).to(torch.bfloat16)
+    y = decode_linear(x.to(gpu), W.to(gpu))
+    ref = (x.float() @ W.float().T).to(torch.bfloat16)
+    _close(y, ref, "plain")
+    # norm prologue from per-16-column partial sums of squares
+    ss = (x.float() ** 2).view(M, K // 16, 16).sum(-1).contiguous()
+    yn = decode_linear(x.to(gpu), W.to(gpu), ss_in=ss.to(gpu), norm_weight=wn.to(gpu), eps=1e-6)
+    refn = (oi.rms_norm(x, wn, 1e-6).float() @ W.float().T).to(torch.bfloat16)
+    torch.cuda.synchronize()
+    _close(yn, refn, "norm prologue")
+
+
+def test_decode_linear_residual_and_silu_epilogues(gpu):
+    from qwen3_engine_from_scratch_amd.kernels.model_ops import decode_linear, embed_ss
+
+    announce("decode_linear residual / silu epilogues, embed_ss")
+    g = torch.Generator().manual_seed(99)
+    M, K, N, I = 48, 2048, 1024, 3072
+    x = torch.randn(M, K, generator=g).to(torch.bfloat16)
+    W = (torch.randn(N, K, generator=g) * 0.05).to(torch.bfloat16)
+    res = (torch.randn(M, N, generator=g) * 2).to(torch.bfloat16)
+    h_out = torch.empty(M, N, dtype=torch.bfloat16, device=gpu)
+    ss_out = torch.empty(M, N // 16, dtype=torch.float32, device=gpu)
+    decode_linear(x.to(gpu), W.to(gpu), epilogue="residual", residual=res.to(gpu),
+                  residual_out=h_out, ss_out=ss_out)
+    o = (x.float() @ W.float().T).to(torch.bfloat16)
+    h_ref = (res.float() + o.float()).to(torch.bfloat16)
+    _close(h_out, h_ref, "residual stream")
+    ss_ref = (h_out.cpu().float() ** 2).view(M, N // 16, 16).sum(-1)
+    torch.testing.assert_close(ss_out.cpu(), ss_ref, rtol=1e-5, atol=0)
+    # repeated calls give the same bits (fixed summation order)
+    for _ in range(3):
+        h2 = torch.empty_like(h_out)
+        ss2 = torch.empty_like(ss_out)
+        decode_linear(x.to(gpu), W.to(gpu), epilogue="residual", residual=res.to(gpu),
+                      residual_out=h2, ss_out=ss2)
+        torch.cuda.synchronize()
+        assert torch.equal(h2, h_out) and torch.equal(ss2, ss_out)
+    # SwiGLU epilogue over a fused gate/up weight
+    Wgu = (torch.randn(2 * I, N, generator=g) * 0.05).to(torch.bfloat16)
+    act = decode_linear(h_out, Wgu.to(gpu), epilogue="silu")
+    gu = (h_out.cpu().float() @ Wgu.float().T).to(torch.bfloat16)
+    act_ref = torch.nn.functional.silu(gu[:, :I]) * gu[:, I:]
+    torch.cuda.synchronize()
+    _close(act, act_ref, "silu epilogue")
+    # embedding rows and their partial sums
+    E = torch.randn(500, 1024, generator=g).to(torch.bfloat16)
+    ids = torch.tensor([3, 499, 0, 500, 7], dtype=torch.int64)
+    h, ss = embed_ss(ids.to(gpu), E.to(gpu))
+    torch.cuda.synchronize()
+    ok = ids < 500
+    assert torch.equal(h.cpu()[ok], E[ids[ok]]) and not h.cpu()[~ok].any()
+    torch.testing.assert_close(ss.cpu()[ok], (E[ids[ok]].float() ** 2).view(-1, 64, 16).sum(-1),
+                               rtol=1e-5, atol=0)
+
+
 # ---- whole model -------------------------------------------------------------
 
 def _tiny(seed=0, layers=2, vocab=2048, hidden=512, inter=1024, hq=4, hkv=2):
@@ -196,6 +276,41 @@ def test_model_prefill_and_decode_vs_oracle(gpu):
         announce(f"  request {i}: rel err {e:.4f} (reference bf16 forward: {e16:.4f})")
         assert e <= max(2 * e16, 0.03), (i, e, e16)
         assert out[0][i, L:].abs().sum() == 0, "pad positions are zero"
+
+
+def test_fused_and_library_decode_paths_agree(gpu):
+    """The fused decode linears and the library-GEMM path compute the same
+    step: both within the model bar of the fp32 oracle, and within bf16
+    noise of each other."""
+    from qwen3_engine_from_scratch_amd.PagedKVcache import PagedKVCache
+
+    model, state, cfg = _tiny(seed=6)
+    model = model.to(gpu)
+    g = torch.Generator().manual_seed(8)
+    lens = [30, 70, 5, 48]
+    seqs = [torch.randint(0, cfg.vocab_size, (L + 1,), generator=g) for L in lens]
+    announce("fused vs library decode step")
+    pool = _pool(cfg, gpu)
+    caches = [PagedKVCache(pool) for _ in lens]
+    for c, sq, L in zip(caches, seqs, lens):
+        model(sq[:L][None].to(gpu), kv_cache=c)
+    for c in caches:
+        c.reserve_next()
+    rows = torch.tensor([c.row_id for c in caches], dtype=torch.int32, device=gpu)
+    ids = torch.stack([sq[L] for sq, L in zip(seqs, lens)]).to(gpu)
+    kb, vb = pool.k_buffer.clone(), pool.v_buffer.clone()
+    fused = model.decode_logits(ids, rows, pool, fused=True).float().cpu()
+    pool.k_buffer.copy_(kb)
+    pool.v_buffer.copy_(vb)
+    lib = model.decode_logits(ids, rows, pool, fused=False).float().cpu()
+    for i, (sq, L) in enumerate(zip(seqs, lens)):
+        ref = om.qwen3_logits_ref(state, cfg, sq)[L]
+        ref16 = om.qwen3_logits_ref(state, cfg, sq, dtype=torch.bfloat16)[L]
+        e16 = _rel(ref16, ref)
+        ef, el = _rel(fused[i], ref), _rel(lib[i], ref)
+        announce(f"  row {i}: fused {ef:.4f} library {el:.4f} reference bf16 {e16:.4f}")
+        assert ef <= max(2 * e16, 0.03) and el <= max(2 * e16, 0.03)
+    assert _rel(fused, lib) < 0.03
 
 
 def test_graph_runner_matches_eager_decode(gpu):
@@ -279,3 +394,21 @@ def test_engine_greedy_generation_vs_oracle(gpu):
         assert gap <= 0.15, (i, gap)
     agree = sum(a == b for x, y in zip(results[True], results[False]) for a, b in zip(x, y))
     assert agree >= 0.9 * sum(new), "graph and eager engines disagree beyond near-ties"
+
+    # eos: a token the model does produce stops each request right after it,
+    # also when it is seen one pipelined step late
+    eos = results[True][2][4]
+    pool = _pool(cfg, gpu, blocks=128, max_requests=32)
+    eng = Engine(model, pool, max_batch=4, use_graph=True)
+    reqs = [GenRequest(i, p, n, eos_token_id=eos) for i, (p, n) in enumerate(zip(prompts, new))]
+    eng.generate(reqs)
+    eng.close()
+    assert pool.free_count == pool.total_blocks, "pages not returned"
+    stopped = 0
+    for r, n in zip(reqs, new):
+        out = r.output_ids
+        assert 1 <= len(out) <= n
+        assert eos not in out[:-1], "tokens generated past eos"
+        assert out[-1] == eos or len(out) == n
+        stopped += out[-1] == eos and len(out) < n
+    assert stopped >= 1, "no request stopped at eos"
