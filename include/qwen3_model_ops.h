@@ -23,6 +23,10 @@
  *   qwen3_embed_ss_bf16     <- the embedding lookup (qwen3/model.py:212) writing
  *                              the residual stream and its partial sums of squares
  *                              for the fused first norm
+ *   qwen3_page_in_bf16      <- the device writes of KVCachePool.alloc (zeroing a
+ *                              reused block, qwen3/PagedKVcache.py:58-73) and of
+ *                              PagedKVCache._allocate_block (the resident table
+ *                              entry, :140-150), for a whole batch in one launch
  *   qwen3_advance_seq_lens  <- the resident-length write of
  *                              PagedKVCache.advance_seq_len
  *                              (qwen3/PagedKVcache.py:216-219), one launch for
@@ -100,6 +104,17 @@ int qwen3_decode_linear_bf16(const void* x, int64_t x_row_stride,
 int qwen3_embed_ss_bf16(const int64_t* ids, const void* embedding,
                         int64_t embedding_row_stride, int64_t vocab, int hidden, int M,
                         void* h_out, int64_t h_row_stride, float* ss_out, void* stream);
+
+/* Maps new pool blocks into the resident block table and zeroes them:
+ * entries holds three int32 arrays of n: rows, then page columns, then block
+ * ids.  block_table[rows[i] * bt_row_stride + cols[i]] = blocks[i] (skipped
+ * when the row or column is out of range) and the block_elems bf16 values of
+ * block blocks[i] in k_cache and in v_cache (the pool's contiguous per-block
+ * chunk: layers x heads x slots x head_dim) are set to zero.  n <= 65535. */
+int qwen3_page_in_bf16(int32_t* block_table, int64_t bt_row_stride, int64_t max_rows,
+                       int64_t max_pages, const int32_t* entries, int n,
+                       void* k_cache, void* v_cache, int64_t block_elems,
+                       int64_t num_blocks, void* stream);
 
 /* seq_lens[row_ids[i]] += delta for i < n, except rows equal to skip_row
  * (a captured batch's padding row) and rows outside [0, max_rows).  Rows

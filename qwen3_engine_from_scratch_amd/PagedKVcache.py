@@ -22,7 +22,7 @@ from . import _lib
 from .kernels.paged_attention import update_kv_batch_hip
 
 __all__ = ["KVCachePool", "PagedKVCache", "prefill_slot_mapping", "write_prefill_batch",
-           "reserve_pages_bulk", "set_seq_lens_bulk"]
+           "reserve_pages_bulk", "set_seq_lens_bulk", "PageIn"]
 
 
 class KVCachePool:
@@ -66,6 +66,16 @@ class KVCachePool:
             idx = torch.tensor(allocated, dtype=torch.long, device=self.k_buffer.device)
             self.k_buffer.index_fill_(0, idx, 0)
             self.v_buffer.index_fill_(0, idx, 0)
+        return allocated
+
+    def take_blocks(self, n: int) -> list:
+        """Pops n block ids like alloc, without touching the device: the
+        caller zeroes them (PageIn does, batched)."""
+        if len(self.free_block_ids) < n:
+            raise RuntimeError(
+                f"OOM: requested {n} blocks, {len(self.free_block_ids)} / {self.total_blocks} free")
+        allocated = self.free_block_ids[-n:]
+        del self.free_block_ids[-n:]
         return allocated
 
     def free(self, block_ids: list):
@@ -196,6 +206,64 @@ class PagedKVCache:
             self.num_pages = 0
         self.seq_len = 0
         self._pool.free_row(self.row_id)
+
+
+class PageIn:
+    """Batched page reservation with no host synchronisation: new blocks are
+    taken on the host, and their table entries plus the zeroing of their K/V
+    go to the device as one asynchronous copy from pinned memory and one
+    launch (qwen3_page_in_bf16).  Two pinned staging buffers alternate, so a
+    buffer is rewritten only after the copy of the call before the previous
+    one has run (the caller synchronises once per step, as the engine does)."""
+
+    def __init__(self, pool: KVCachePool, capacity: int):
+        assert pool.k_buffer.is_contiguous() and pool.v_buffer.is_contiguous()
+        self.pool = pool
+        self.cap = capacity
+        self._host = [torch.empty(3 * capacity, dtype=torch.int32, pin_memory=True)
+                      for _ in range(2)]
+        self._dev = torch.empty(3 * capacity, dtype=torch.int32, device=pool.k_buffer.device)
+        self._flip = 0
+
+    def reserve(self, caches, tokens) -> int:
+        """Gives every handle enough pages for tokens[i] tokens; returns the
+        number of blocks mapped."""
+        pool = self.pool
+        bs = pool.block_size
+        max_pages = pool.block_table_2d.shape[1]
+        want = []
+        for c, n in zip(caches, tokens):
+            k = (int(n) + bs - 1) // bs - c.num_pages
+            if k > 0:
+                assert c.num_pages + k <= max_pages, \
+                    f"request exceeds max_seq_len ({pool.max_seq_len} tokens / {max_pages} pages)"
+                want.append((c, k))
+        total = sum(k for _, k in want)
+        if total == 0:
+            return 0
+        assert total <= self.cap, f"{total} new pages in one step (staging holds {self.cap})"
+        ids = pool.take_blocks(total)
+        h = self._host[self._flip]
+        self._flip ^= 1
+        i = 0
+        for c, k in want:
+            for j in range(k):
+                h[i] = c.row_id
+                h[total + i] = c.num_pages + j
+                h[2 * total + i] = ids[i]
+                i += 1
+            c.block_table.extend(ids[i - k:i])
+            c.num_pages += k
+        d = self._dev[:3 * total]
+        d.copy_(h[:3 * total], non_blocking=True)
+        bt = pool.block_table_2d
+        kb = pool.k_buffer
+        rc = _lib.load().qwen3_page_in_bf16(
+            bt.data_ptr(), bt.stride(0), bt.shape[0], bt.shape[1], d.data_ptr(), total,
+            kb.data_ptr(), pool.v_buffer.data_ptr(), kb[0].numel(), kb.shape[0],
+            _lib.stream_of(kb.device))
+        _lib.check(rc, "qwen3_page_in_bf16")
+        return total
 
 
 def reserve_pages_bulk(caches, tokens: list) -> None:

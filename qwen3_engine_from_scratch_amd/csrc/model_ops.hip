@@ -1,7 +1,8 @@
 // Row-wise model kernels around the attention path of a Qwen3 decoder step:
 // fused residual add + RMSNorm (also the embedding lookup and the final-norm
-// row selection), SiLU * up of the MLP, greedy (argmax) token selection, and
-// the device-side advance of the resident sequence lengths.
+// row selection), SiLU * up of the MLP, greedy (argmax) token selection, the
+// device-side advance of the resident sequence lengths, and the batched
+// page-in (table entries + zeroing) of newly allocated pool blocks.
 //
 // Arithmetic and roundings follow the reference modules:
 //   residual add (qwen3/decoder.py:49,55):   h = bf16(residual + x)
@@ -199,7 +200,55 @@ __global__ void advance_kernel(int32_t* seq_lens, int64_t max_rows, const int32_
   seq_lens[r] += delta;
 }
 
+// Page-in of newly allocated pool blocks: entry i (rows[i], cols[i],
+// blocks[i]) maps page cols[i] of resident-table row rows[i] to block
+// blocks[i], whose K and V contents (every layer and head) are zeroed.
+// Grid: (chunks of a block, entries, K/V).
+constexpr int kPageThreads = 256;
+
+__global__ __launch_bounds__(kPageThreads) void page_in_kernel(
+    int32_t* table, int64_t stride, int64_t max_rows, int64_t max_pages,
+    const int32_t* entries, int n, uint16_t* k_cache, uint16_t* v_cache, int64_t block_elems,
+    int64_t num_blocks) {
+  const int i = blockIdx.y;
+  const int64_t row = entries[i], col = entries[n + i], blk = entries[2 * n + i];
+  if (blk < 0 || blk >= num_blocks) return;
+  if (blockIdx.x == 0 && blockIdx.z == 0 && threadIdx.x == 0 && row >= 0 && row < max_rows &&
+      col >= 0 && col < max_pages)
+    table[row * stride + col] = static_cast<int32_t>(blk);
+  uint16_t* base = (blockIdx.z == 0 ? k_cache : v_cache) + blk * block_elems;
+  const int64_t chunks = block_elems / 8;
+  const q3::u32x4 z = {0u, 0u, 0u, 0u};
+  for (int64_t c = static_cast<int64_t>(blockIdx.x) * kPageThreads + threadIdx.x; c < chunks;
+       c += static_cast<int64_t>(gridDim.x) * kPageThreads)
+    q3::st16(base + 8 * c, z);
+}
+
 }  // namespace
+
+extern "C" int qwen3_page_in_bf16(int32_t* block_table, int64_t bt_row_stride, int64_t max_rows,
+                                  int64_t max_pages, const int32_t* entries, int n,
+                                  void* k_cache, void* v_cache, int64_t block_elems,
+                                  int64_t num_blocks, void* stream) {
+  const char* who = "qwen3_page_in_bf16";
+  if (!block_table || !entries || !k_cache || !v_cache)
+    return q3::fail(QWEN3_EINVAL, "%s: null pointer argument", who);
+  if (n < 0 || n > 65535 || max_rows <= 0 || max_pages <= 0 || bt_row_stride < max_pages ||
+      block_elems <= 0 || num_blocks <= 0)
+    return q3::fail(QWEN3_EINVAL, "%s: bad sizes", who);
+  if (block_elems % 8 != 0 || !q3::aligned16(k_cache) || !q3::aligned16(v_cache))
+    return q3::fail(QWEN3_EALIGN, "%s: blocks must be whole 16-byte chunks", who);
+  if (n == 0) return QWEN3_OK;
+  const int64_t chunks = block_elems / 8;
+  const unsigned gx = static_cast<unsigned>(
+      q3::cdiv(chunks, kPageThreads) < 64 ? q3::cdiv(chunks, kPageThreads) : 64);
+  q3::clear_error();
+  hipLaunchKernelGGL(page_in_kernel, dim3(gx, static_cast<unsigned>(n), 2), dim3(kPageThreads), 0,
+                     static_cast<hipStream_t>(stream), block_table, bt_row_stride, max_rows,
+                     max_pages, entries, n, static_cast<uint16_t*>(k_cache),
+                     static_cast<uint16_t*>(v_cache), block_elems, num_blocks);
+  return q3::launch_status(who);
+}
 
 extern "C" int qwen3_add_rms_norm_bf16(const void* x, int64_t x_row_stride, const void* residual,
                                        int64_t residual_row_stride, void* residual_out,

@@ -15,8 +15,8 @@ the per-step state lives:
     whose resident seq_lens advance on the device, so an unchanged batch
     needs no host->device copy at all; a changed batch copies its ids and
     rows once;
-  - pages for the next token are reserved for the whole batch with one pool
-    allocation and one block-table write (reserve_pages_bulk);
+  - pages for the next token are reserved for the whole batch with one
+    asynchronous copy and one launch that maps and zeroes them (PageIn);
   - the host reads back only the B new token ids per step, and does so
     after it has launched the next step (whose inputs are already on the
     device), so its bookkeeping overlaps the GPU.  A request's count limit
@@ -33,7 +33,7 @@ from dataclasses import dataclass, field
 import numpy as np
 import torch
 
-from .PagedKVcache import PagedKVCache, reserve_pages_bulk, set_seq_lens_bulk
+from .PagedKVcache import PageIn, PagedKVCache, set_seq_lens_bulk
 from .graph_runner import GraphRunner, pow2_buckets
 from .kernels.model_ops import argmax
 
@@ -85,6 +85,8 @@ class Engine:
         self._tok_host = [torch.empty(max(max_batch, 1), dtype=torch.int64, pin_memory=True)
                           for _ in range(2)]
         self._flip = 0
+        max_pages = pool.block_table_2d.shape[1]
+        self._pages = PageIn(pool, max(max_batch * max_pages, 64))
         self._pending = None     # (requests, host view, event) of the last decode launch
         self._last_batch = None  # (bucket, request ids) of the last graph replay
 
@@ -95,7 +97,7 @@ class Engine:
         lens = [len(r.prompt) for r in reqs]
         for r in reqs:
             r.cache = PagedKVCache(self.pool)
-        reserve_pages_bulk([r.cache for r in reqs], lens)
+        self._pages.reserve([r.cache for r in reqs], lens)
         n = len(reqs)
         cu = np.zeros(n + 1, dtype=np.int64)
         cu[1:] = np.cumsum(lens)
@@ -156,7 +158,7 @@ class Engine:
             self._drain()
         caches = [r.cache for r in reqs]
         # the token of this step lands at position seq_len: reserve its page
-        reserve_pages_bulk(caches, [c.seq_len + 1 for c in caches])
+        self._pages.reserve(caches, [c.seq_len + 1 for c in caches])
         if self.runner is not None:
             if key == self._last_batch:
                 out = self.runner.replay_greedy(k)

@@ -215,6 +215,32 @@ def test_decode_linear_residual_and_silu_epilogues(gpu):
                                rtol=1e-5, atol=0)
 
 
+def test_page_in_maps_and_zeroes_blocks(gpu):
+    from qwen3_engine_from_scratch_amd.PagedKVcache import KVCachePool, PageIn, PagedKVCache
+
+    announce("page-in: batched table entries + block zeroing")
+    pool = KVCachePool(20, 3, 16, 2, 128, device=gpu, dtype=torch.bfloat16, max_seq_len=256,
+                       max_requests=8)
+    pool.k_buffer.fill_(1.0)
+    pool.v_buffer.fill_(2.0)
+    caches = [PagedKVCache(pool) for _ in range(3)]
+    pages = PageIn(pool, capacity=32)
+    assert pages.reserve(caches, [17, 0, 40]) == 2 + 0 + 3
+    assert pages.reserve(caches, [17, 1, 48]) == 0 + 1 + 0
+    torch.cuda.synchronize()
+    bt = pool.block_table_2d.cpu()
+    used = []
+    for c in caches:
+        assert bt[c.row_id, :c.num_pages].tolist() == c.block_table
+        assert (bt[c.row_id, c.num_pages:] == -1).all()
+        used += c.block_table
+    kb, vb = pool.k_buffer.cpu(), pool.v_buffer.cpu()
+    mask = torch.zeros(20, dtype=torch.bool)
+    mask[used] = True
+    assert not kb[mask].any() and not vb[mask].any(), "new blocks zeroed"
+    assert (kb[~mask] == 1.0).all() and (vb[~mask] == 2.0).all(), "other blocks untouched"
+
+
 # ---- whole model -------------------------------------------------------------
 
 def _tiny(seed=0, layers=2, vocab=2048, hidden=512, inter=1024, hq=4, hkv=2):
