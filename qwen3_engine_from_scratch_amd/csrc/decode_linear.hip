@@ -15,14 +15,16 @@
 // Weights are nn.Linear's (N x K) row-major matrices, y = a @ W^T.
 //
 // Work split: one workgroup per (16 output columns, 16 rows) block (32
-// columns for kSilu: the gate and up tiles of the same columns); its four
-// waves (eight when K >= 2048) take an equal share of K each and stream their weight rows
-// straight from HBM as the B operand of mfma_f32_16x16x32_bf16, with two
-// register buffers of loads in flight, and the four partial tiles are summed
-// through LDS in wave order, so results are reproducible bit for bit.  The
-// row blocks of one column tile are placed on the same XCD (workgroups are
-// dealt to the 8 XCDs round-robin), so the tile's weights come from HBM once
-// and from that XCD's L2 for the other row blocks.
+// columns for kSilu: the gate and up tiles of the same columns).  Its four
+// waves (eight when K >= 2048) take an equal share of K each and stream
+// their weight rows straight from HBM as the B operand of
+// mfma_f32_16x16x32_bf16, with two register buffers of loads in flight.
+// Loads are coalesced (a lane quad reads one row's 64-byte k-step) and
+// redistributed into the operand layout with ds_bpermute.  The partial tiles
+// are summed through LDS in wave order, so results are reproducible bit for
+// bit.  The row blocks of one column tile are placed on the same XCD
+// (workgroups are dealt to the 8 XCDs round-robin), so the tile's weights
+// come from HBM once and from that XCD's L2 for the other row blocks.
 #include "common.hpp"
 
 namespace {
@@ -30,6 +32,7 @@ namespace {
 constexpr int kMaxRows = 64;
 constexpr int kTile = 16;         // output columns per tile
 constexpr int kKStep = 32;        // k per MFMA
+constexpr int kMaxNormK = 8192;  // widest input a norm prologue stages in LDS
 constexpr int kXcds = 8;          // XCDs of an MI355X; workgroup b runs on XCD b % 8
 
 enum Epi : int { kStore = 0, kResidual = 1, kSilu = 2 };
@@ -65,6 +68,7 @@ __global__ __launch_bounds__(kWaves * 64) void decode_linear_kernel(LinArgs a) {
   constexpr int kC = 4;                         // k-steps per prefetch buffer
   __shared__ float rms_s[16];
   __shared__ float red[kWaves][kCols][4][64];
+  __shared__ q3::u32x4 nw_s[kNorm ? kMaxNormK / 8 : 1];  // norm weight, staged once
 
   // (tile, row block) of this workgroup: the rbc row blocks of a tile share
   // one XCD (block b runs on XCD b % 8).
@@ -84,20 +88,31 @@ __global__ __launch_bounds__(kWaves * 64) void decode_linear_kernel(LinArgs a) {
   const int k0 = wave * kw;
   const int steps = kw / kKStep;
 
+  // Loads are coalesced: the four lanes of a quad read one row's 64 bytes of
+  // a k-step (lane l: row l / 4, k-group l % 4).  The MFMA operands want
+  // lane L to hold row L % 16, k-group L / 16, so every loaded vector is
+  // redistributed with ds_bpermute: lane L takes lane 4 * (L % 16) + L / 16.
+  const int lrow = lane >> 2, lkg = 8 * (lane & 3);
+  const int perm_addr = 4 * (4 * r16 + (lane >> 4));
   const uint16_t* wrow[kCols];
-  wrow[0] = a.w + static_cast<int64_t>(n0 + r16) * a.w_s + kg + k0;
+  wrow[0] = a.w + static_cast<int64_t>(n0 + lrow) * a.w_s + lkg + k0;
   if constexpr (kCols == 2)
-    wrow[1] = a.w + static_cast<int64_t>(a.up_row + n0 + r16) * a.w_s + kg + k0;
-  const int xr = min(rb * 16 + r16, a.M - 1);  // rows past M repeat the last row
-  const uint16_t* xrow = a.x + static_cast<int64_t>(xr) * a.x_s + kg + k0;
-  const uint16_t* nwp = kNorm ? a.norm_w + kg + k0 : nullptr;
+    wrow[1] = a.w + static_cast<int64_t>(a.up_row + n0 + lrow) * a.w_s + lkg + k0;
+  const int xr = min(rb * 16 + lrow, a.M - 1);  // rows past M repeat the last row
+  const uint16_t* xrow = a.x + static_cast<int64_t>(xr) * a.x_s + lkg + k0;
+  auto to_mfma = [&](q3::u32x4 v) {
+    q3::u32x4 o;
+#pragma unroll
+    for (int e = 0; e < 4; ++e)
+      o[e] = static_cast<uint32_t>(__builtin_amdgcn_ds_bpermute(perm_addr, static_cast<int>(v[e])));
+    return o;
+  };
 
   // Two register buffers of kC k-steps: the loads of one are in flight while
   // the other feeds the MFMAs.
   struct Buf {
     q3::u32x4 b[kC][kCols];
     q3::u32x4 x[kC];
-    q3::u32x4 nw[kC];
   };
   auto load = [&](Buf& B, int s0) {
 #pragma unroll
@@ -107,12 +122,14 @@ __global__ __launch_bounds__(kWaves * 64) void decode_linear_kernel(LinArgs a) {
 #pragma unroll
       for (int c = 0; c < kCols; ++c) B.b[u][c] = q3::ld16(wrow[c] + k);
       B.x[u] = q3::ld16(xrow + k);
-      if constexpr (kNorm) B.nw[u] = q3::ld16(nwp + k);
     }
   };
   Buf p, q;
   load(p, 0);
   load(q, kC);
+  if constexpr (kNorm) {
+    for (int i = threadIdx.x; i < a.K / 8; i += kWaves * 64) nw_s[i] = q3::ld16(a.norm_w + 8 * i);
+  }
 
   float rms = 0.f;
   if constexpr (kNorm) {
@@ -149,16 +166,17 @@ __global__ __launch_bounds__(kWaves * 64) void decode_linear_kernel(LinArgs a) {
 #pragma unroll
     for (int u = 0; u < kC; ++u) {
       if (s0 + u >= steps) break;
-      q3::u32x4 av = B.x[u];
+      q3::u32x4 av = to_mfma(B.x[u]);
       if constexpr (kNorm) {
+        const q3::u32x4 nw = nw_s[(k0 + kg + (s0 + u) * kKStep) >> 3];
 #pragma unroll
         for (int e = 0; e < 4; ++e)
-          av[e] = q3::pack_bf16x2((q3::bf16_lo(av[e]) * rms) * q3::bf16_lo(B.nw[u][e]),
-                                  (q3::bf16_hi(av[e]) * rms) * q3::bf16_hi(B.nw[u][e]));
+          av[e] = q3::pack_bf16x2((q3::bf16_lo(av[e]) * rms) * q3::bf16_lo(nw[e]),
+                                  (q3::bf16_hi(av[e]) * rms) * q3::bf16_hi(nw[e]));
       }
 #pragma unroll
       for (int c = 0; c < kCols; ++c)
-        acc[c] = q3::mfma16x16x32(q3::as_bf16x8(av), q3::as_bf16x8(B.b[u][c]), acc[c]);
+        acc[c] = q3::mfma16x16x32(q3::as_bf16x8(av), q3::as_bf16x8(to_mfma(B.b[u][c])), acc[c]);
     }
   };
   for (int s0 = 0; s0 < steps; s0 += 2 * kC) {
@@ -272,6 +290,8 @@ extern "C" int qwen3_decode_linear_bf16(const void* x, int64_t x_row_stride, con
   const bool norm = ss_in != nullptr;
   if (norm && (!norm_weight || ss_in_tiles <= 0 || !(eps >= 0.f)))
     return q3::fail(QWEN3_EINVAL, "%s: the norm prologue needs its weight and partial sums", who);
+  if (norm && K > kMaxNormK)
+    return q3::fail(QWEN3_EUNSUPPORTED, "%s: a norm prologue supports K <= %d", who, kMaxNormK);
   if ((epilogue != kResidual && !y) ||
       (epilogue == kResidual && (!residual || !residual_out || !ss_out)))
     return q3::fail(QWEN3_EINVAL, "%s: null output for this epilogue", who);
