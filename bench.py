@@ -1,7 +1,7 @@
 """Benchmark of the MI355X attention hot path.
 
     python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu-baseline]
-                    [--only decode|prefill|pre_attention|e2e] [--workload config3|config4]
+                    [--only decode|prefill|pre_attention|sampling|e2e] [--workload config3|config4]
 
 Headline (the JSON `value`): paged decode attention at the Qwen3-8B shape —
 batch 256, 32 query / 8 KV heads, head_dim 128, bf16, block 16, context
@@ -21,6 +21,8 @@ Also reported on the same line:
                 the 2.5 PFLOP/s bf16 dense MFMA peak, plus its slot write;
   pre_attention the fused QK-RMSNorm + RoPE + pool write (prefill and decode
                 forms) against the HBM peak;
+  sampling      greedy and top-k / top-p token sampling over a 64 x 151936
+                batch of logits, per call;
   e2e           the whole Qwen3-0.6B model (random-init bf16) serving 64
                 requests by continuous batching, 256 greedy tokens each, in
                 output tokens/s.
@@ -377,6 +379,31 @@ def bench_prefill(args, dev):
                            "ms_per_step": round(w_evt, 5), "bytes": wbytes}}
 
 
+def bench_sampling(args, dev):
+    """Token sampling over one decode batch of Qwen3 logits (B=64 rows x
+    151936 bf16): greedy (argmax kernel) and temperature 0.8 / top-k 50 /
+    top-p 0.9 (the sampling kernel), per call; bytes = one read of the
+    logits (the sampler re-reads them from L2 in its later passes)."""
+    import torch
+
+    from qwen3_engine_from_scratch_amd.sampling import sample_tokens
+
+    B, V = 64, 151936
+    g = torch.Generator(device=dev).manual_seed(0)
+    x = (torch.randn(B, V, device=dev, generator=g) * 2).to(torch.bfloat16)
+    t = torch.full((B,), 0.8, device=dev)
+    k = torch.full((B,), 50, device=dev, dtype=torch.int32)
+    p = torch.full((B,), 0.9, device=dev)
+    res = {"workload": f"B={B} rows x {V} bf16 logits", "bytes": B * V * 2}
+    for name, fn in (("greedy", lambda: sample_tokens(x)),
+                     ("top_k50_top_p0.9_T0.8", lambda: sample_tokens(x, t, k, p, seed=1))):
+        _, ms = time_steps(fn, args.steps, args.warmup)
+        res[name] = {"us_per_call": round(ms * 1e3, 2),
+                     "GB/s": round(B * V * 2 / (ms * 1e-3) / 1e9, 1)}
+        log(f"sampling {name}: {ms * 1e3:.1f} us/call")
+    return res
+
+
 def bench_e2e(args, dev):
     """Whole Qwen3-0.6B (random-init bf16 weights) serving 64 requests with
     continuous batching: prompts of seeded lengths uniform in [128, 1024],
@@ -447,7 +474,7 @@ def main(argv=None):
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--no-cpu-baseline", action="store_true")
-    ap.add_argument("--only", choices=["decode", "prefill", "pre_attention", "e2e"],
+    ap.add_argument("--only", choices=["decode", "prefill", "pre_attention", "sampling", "e2e"],
                     default=None)
     ap.add_argument("--e2e-tokens", type=int, default=256,
                     help="greedy tokens per request in the whole-model serving line")
@@ -536,6 +563,9 @@ def main(argv=None):
             line.update(value=pf["value"], unit=pf["unit"], ms_per_step=pf["ms_per_step"],
                         config={"workload": pf["workload"]}, roofline=pf["roofline"])
         line["prefill"] = pf
+        torch.cuda.empty_cache()
+    if args.only in (None, "sampling"):
+        line["sampling"] = bench_sampling(args, dev)
         torch.cuda.empty_cache()
     if args.only in (None, "e2e"):
         e2e = bench_e2e(args, dev)

@@ -27,6 +27,10 @@
  *                              reused block, qwen3/PagedKVcache.py:58-73) and of
  *                              PagedKVCache._allocate_block (the resident table
  *                              entry, :140-150), for a whole batch in one launch
+ *   qwen3_sample_bf16       <- sample_tokens (qwen3/sampling.py:234-270) with the
+ *                              fused top-p / Gumbel-max kernel of its fast path
+ *                              (:112-178) and its torch fallback (:76-108):
+ *                              temperature, top-k, top-p per row in one launch
  *   qwen3_advance_seq_lens  <- the resident-length write of
  *                              PagedKVCache.advance_seq_len
  *                              (qwen3/PagedKVcache.py:216-219), one launch for
@@ -115,6 +119,22 @@ int qwen3_page_in_bf16(int32_t* block_table, int64_t bt_row_stride, int64_t max_
                        int64_t max_pages, const int32_t* entries, int n,
                        void* k_cache, void* v_cache, int64_t block_elems,
                        int64_t num_blocks, void* stream);
+
+/* Samples one token per row of bf16 logits (out[r], int64), per-row
+ * parameters as device arrays (NULL: temperature 0, top_k 0, top_p 1):
+ *   temperature[r] <= 0  the first index of the largest logit (NaN highest);
+ *   otherwise            among the top_k[r] largest logits (all when
+ *                        top_k[r] <= 0 or > vocab), sorted descending with
+ *                        ties by lower index, the leading positions whose
+ *                        softmax(logit / temperature) mass before them is
+ *                        <= top_p[r] (the first always), a token is drawn
+ *                        with probability proportional to
+ *                        exp(logit / temperature) (Gumbel-max over the kept
+ *                        tokens; Philox4x32-10 keyed by seed and row).
+ * NaN logits are never drawn.  One 1024-thread workgroup per row. */
+int qwen3_sample_bf16(const void* logits, int64_t row_stride, int64_t rows, int64_t vocab,
+                      const float* temperature, const int32_t* top_k, const float* top_p,
+                      uint64_t seed, int64_t* out, void* stream);
 
 /* seq_lens[row_ids[i]] += delta for i < n, except rows equal to skip_row
  * (a captured batch's padding row) and rows outside [0, max_rows).  Rows

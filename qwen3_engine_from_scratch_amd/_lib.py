@@ -82,6 +82,7 @@ _SIGNATURES = {
     "qwen3_argmax_bf16": (_i, [_vp, _i64, _i64, _i64, _vp, _vp]),
     "qwen3_advance_seq_lens": (_i, [_vp, _i64, _vp, _i, _i, _i, _vp]),
     "qwen3_page_in_bf16": (_i, [_vp, _i64, _i64, _i64, _vp, _i, _vp, _vp, _i64, _i64, _vp]),
+    "qwen3_sample_bf16": (_i, [_vp, _i64, _i64, _i64, _vp, _vp, _vp, ctypes.c_uint64, _vp, _vp]),
     "qwen3_decode_linear_bf16": (
         _i,
         [_vp, _i64, _vp, _i, _vp, ctypes.c_float, _vp, _i64, _i, _i, _i, _i,

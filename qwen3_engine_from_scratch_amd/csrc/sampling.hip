@@ -1,0 +1,429 @@
+// Token sampling on the GPU: temperature, top-k, top-p and a categorical
+// draw per row of bf16 logits, the rule of sample_tokens
+// (qwen3/sampling.py:112-178, 234-270):
+//   temperature <= 0     greedy: the first index of the largest logit
+//   otherwise            x = logit / temperature over the k largest logits
+//                        (k = top_k, or all when top_k <= 0), sorted
+//                        descending; position j is kept while the softmax
+//                        mass before it is <= top_p (position 0 always);
+//                        the token is argmax over kept positions of
+//                        x + Gumbel noise, i.e. a draw from softmax(x)
+//                        restricted to them.
+// Ties in value are ordered by token index (lower first).  The random
+// stream is this file's own (Philox4x32-10 keyed by seed and row, counter =
+// token index), so draws are reproducible for a seed but are not the
+// reference's stream; the distribution is the same.
+//
+// One 1024-thread workgroup per row, passes over the row (L2-resident after
+// the first):
+//   A  count histogram of the high byte of the 16-bit order-preserving key,
+//      and the maximum key
+//   B  count histogram of the low byte inside the top-k boundary bin -> the
+//      exact k-th largest key and how many of its ties are kept
+//   C  softmax mass histogram (high byte) of the top-k set, and its total
+//   D  low-byte mass histogram inside the top-p boundary bin -> the exact
+//      top-p cut
+//   E  Gumbel-max over the kept tokens
+// Masses are summed as 64-bit fixed point (2^40 per unit), so every
+// histogram and the cut are independent of summation order.
+#include "common.hpp"
+
+namespace {
+
+constexpr int kThreads = 1024;
+constexpr int kWaves = kThreads / 64;
+constexpr double kFix = 1099511627776.0;  // 2^40
+
+// Order-preserving 16-bit key of a bf16 value (larger value, larger key);
+// NaN maps below every number, so it is never sampled.
+__device__ __forceinline__ uint32_t okey(uint32_t b) {
+  if ((b & 0x7F80u) == 0x7F80u && (b & 0x7Fu)) return 0u;
+  return (b & 0x8000u) ? (~b & 0xFFFFu) : (b | 0x8000u);
+}
+__device__ __forceinline__ float key_value(uint32_t key) {
+  const uint32_t b = (key & 0x8000u) ? (key & 0x7FFFu) : (~key & 0xFFFFu);
+  return __uint_as_float(b << 16);
+}
+
+// Philox4x32-10 (Salmon, Moraes, Dror, Shaw, "Parallel random numbers: as
+// easy as 1, 2, 3", SC 2011): 10 rounds of the published multipliers and
+// Weyl key increments.
+__device__ __forceinline__ uint32_t mulhilo(uint32_t a, uint32_t b, uint32_t& hi) {
+  const uint64_t p = static_cast<uint64_t>(a) * b;
+  hi = static_cast<uint32_t>(p >> 32);
+  return static_cast<uint32_t>(p);
+}
+__device__ __forceinline__ uint32_t philox_first(uint32_t c0, uint32_t c1, uint32_t c2,
+                                                 uint32_t c3, uint32_t k0, uint32_t k1) {
+#pragma unroll
+  for (int r = 0; r < 10; ++r) {
+    uint32_t hi0, hi1;
+    const uint32_t lo0 = mulhilo(0xD2511F53u, c0, hi0);
+    const uint32_t lo1 = mulhilo(0xCD9E8D57u, c2, hi1);
+    const uint32_t n0 = hi1 ^ c1 ^ k0, n1 = lo1, n2 = hi0 ^ c3 ^ k1, n3 = lo0;
+    c0 = n0, c1 = n1, c2 = n2, c3 = n3;
+    k0 += 0x9E3779B9u;
+    k1 += 0xBB67AE85u;
+  }
+  return c0;
+}
+// Standard Gumbel noise of token i of a row: u in (0, 1), g = -log(-log u).
+__device__ __forceinline__ float gumbel(uint64_t seed, int64_t row, int64_t i) {
+  const uint32_t r = philox_first(static_cast<uint32_t>(i), static_cast<uint32_t>(i >> 32),
+                                  static_cast<uint32_t>(row), 0x5EED5EEDu,
+                                  static_cast<uint32_t>(seed), static_cast<uint32_t>(seed >> 32));
+  const float u = (static_cast<float>(r >> 8) + 0.5f) * (1.f / 16777216.f);
+  return -logf(-logf(u));
+}
+
+struct Shared {
+  uint32_t cnt[256];
+  unsigned long long mass[256];
+  int wsum[kWaves];
+  unsigned long long wmass[kWaves];
+  uint32_t wmax[kWaves];
+  unsigned long long best[kWaves];
+};
+
+// Block-wide sums; every thread gets the result.
+__device__ __forceinline__ int block_sum_int(int v, Shared& sh) {
+#pragma unroll
+  for (int m = 1; m < 64; m <<= 1) v += __shfl_xor(v, m, 64);
+  __syncthreads();
+  if ((threadIdx.x & 63) == 0) sh.wsum[threadIdx.x >> 6] = v;
+  __syncthreads();
+  int t = 0;
+#pragma unroll
+  for (int w = 0; w < kWaves; ++w) t += sh.wsum[w];
+  return t;
+}
+
+// Exclusive block scan of per-thread counts in thread order; also returns
+// the total.
+__device__ __forceinline__ int block_scan_int(int v, int& total, Shared& sh) {
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  int incl = v;
+#pragma unroll
+  for (int o = 1; o < 64; o <<= 1) {
+    const int y = __shfl_up(incl, o, 64);
+    if (lane >= o) incl += y;
+  }
+  __syncthreads();
+  if (lane == 63) sh.wsum[wave] = incl;
+  __syncthreads();
+  int before = 0;
+  total = 0;
+#pragma unroll
+  for (int w = 0; w < kWaves; ++w) {
+    if (w < wave) before += sh.wsum[w];
+    total += sh.wsum[w];
+  }
+  return before + incl - v;
+}
+
+// Visits the row in rounds of kThreads * 8 tokens: thread t gets tokens
+// base + 8t .. base + 8t + 7 of each round (16-byte loads when aligned).
+template <bool kVec, typename F>
+__device__ __forceinline__ void for_each_round(const uint16_t* p, int64_t vocab, F&& f) {
+  const int64_t per_round = static_cast<int64_t>(kThreads) * 8;
+  for (int64_t base = 0; base < vocab; base += per_round) {
+    const int64_t i0 = base + 8 * static_cast<int64_t>(threadIdx.x);
+    uint32_t b[8];
+    if (kVec && i0 + 8 <= vocab) {
+      const q3::u32x4 v = q3::ld16(p + i0);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        b[2 * e] = v[e] & 0xFFFFu;
+        b[2 * e + 1] = v[e] >> 16;
+      }
+    } else {
+#pragma unroll
+      for (int e = 0; e < 8; ++e) b[e] = i0 + e < vocab ? p[i0 + e] : 0x7FC1u;  // NaN pad
+    }
+    f(i0, b);
+  }
+}
+
+// Scans a 256-bin count histogram from the top: returns the bin where the
+// running count (starting at `above`) first reaches `need`, and the count
+// strictly above that bin.
+__device__ __forceinline__ int find_count_bin(const uint32_t* h, int64_t need, int64_t& above) {
+  int64_t run = above;
+  for (int bin = 255; bin >= 0; --bin) {
+    if (run + h[bin] >= need) {
+      above = run;
+      return bin;
+    }
+    run += h[bin];
+  }
+  above = run;
+  return 0;
+}
+
+template <bool kVec>
+__global__ __launch_bounds__(kThreads) void sample_kernel(const uint16_t* logits, int64_t row_s,
+                                                          int64_t vocab, const float* temperature,
+                                                          const int32_t* top_k,
+                                                          const float* top_p, uint64_t seed,
+                                                          int64_t* out) {
+  __shared__ Shared sh;
+  const int64_t row = blockIdx.x;
+  const uint16_t* p = logits + row * row_s;
+  const float temp = temperature ? temperature[row] : 0.f;
+  const int tid = threadIdx.x;
+  const int lane = tid & 63, wave = tid >> 6;
+
+  // ---- greedy -----------------------------------------------------------
+  if (!(temp > 0.f)) {
+    // first index of the largest value; NaN ranks highest, as torch.argmax
+    unsigned long long bestk = 0;
+    for_each_round<kVec>(p, vocab, [&](int64_t i0, const uint32_t* b) {
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        if (i0 + e >= vocab) break;
+        const uint32_t bb = b[e];
+        const bool nan = (bb & 0x7F80u) == 0x7F80u && (bb & 0x7Fu);
+        const uint32_t k = nan ? 0x10000u : okey(bb);
+        const unsigned long long key =
+            (static_cast<unsigned long long>(k + 1) << 32) | (~static_cast<uint32_t>(i0 + e));
+        bestk = key > bestk ? key : bestk;
+      }
+    });
+#pragma unroll
+    for (int m = 1; m < 64; m <<= 1) {
+      const unsigned long long o = __shfl_xor(bestk, m, 64);
+      bestk = o > bestk ? o : bestk;
+    }
+    if (lane == 0) sh.best[wave] = bestk;
+    __syncthreads();
+    if (tid == 0) {
+      unsigned long long b = 0;
+      for (int w = 0; w < kWaves; ++w) b = sh.best[w] > b ? sh.best[w] : b;
+      out[row] = static_cast<int64_t>(~static_cast<uint32_t>(b));
+    }
+    return;
+  }
+
+  const int64_t kreq = top_k ? top_k[row] : 0;
+  const int64_t k = (kreq <= 0 || kreq > vocab) ? vocab : kreq;
+  const float pcut = top_p ? top_p[row] : 1.f;
+  const bool use_p = pcut < 1.f;
+  const float inv_t = 1.f / temp;
+
+  // ---- A: high-byte counts and the maximum key --------------------------
+  for (int i = tid; i < 256; i += kThreads) sh.cnt[i] = 0;
+  __syncthreads();
+  uint32_t kmax = 0;
+  for_each_round<kVec>(p, vocab, [&](int64_t i0, const uint32_t* b) {
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      if (i0 + e >= vocab) break;
+      const uint32_t key = okey(b[e]);
+      kmax = key > kmax ? key : kmax;
+      atomicAdd(&sh.cnt[key >> 8], 1u);
+    }
+  });
+#pragma unroll
+  for (int m = 1; m < 64; m <<= 1) {
+    const uint32_t o = __shfl_xor(kmax, m, 64);
+    kmax = o > kmax ? o : kmax;
+  }
+  if (lane == 0) sh.wmax[wave] = kmax;
+  __syncthreads();
+  kmax = 0;
+#pragma unroll
+  for (int w = 0; w < kWaves; ++w) kmax = sh.wmax[w] > kmax ? sh.wmax[w] : kmax;
+  const float xmax = key_value(kmax) * inv_t;
+
+  // ---- B: exact k-th largest key (kk) and the ties of it kept (tk) ------
+  uint32_t kk = 0;  // every key >= 0: with k == vocab nothing is cut
+  int64_t tk = 0, kties = 0;
+  if (k < vocab) {
+    int64_t above = 0;
+    const int hb = find_count_bin(sh.cnt, k, above);
+    __syncthreads();
+    for (int i = tid; i < 256; i += kThreads) sh.cnt[i] = 0;
+    __syncthreads();
+    for_each_round<kVec>(p, vocab, [&](int64_t i0, const uint32_t* b) {
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        if (i0 + e >= vocab) break;
+        const uint32_t key = okey(b[e]);
+        if (static_cast<int>(key >> 8) == hb) atomicAdd(&sh.cnt[key & 0xFF], 1u);
+      }
+    });
+    __syncthreads();
+    const int lb = find_count_bin(sh.cnt, k, above);
+    kk = (static_cast<uint32_t>(hb) << 8) | static_cast<uint32_t>(lb);
+    kties = sh.cnt[lb];
+    tk = k - above;  // 1 <= tk <= kties
+  }
+  // membership in the top-k list before tie ranks: key > kk, or key == kk
+  // with rank < tk (ranks in token order)
+
+  // ---- C, D: the top-p cut over the top-k list ---------------------------
+  // kc / tc: the final cut (key and ties kept at it); the kept list is the
+  // first min(k, n_p) positions of the sorted top-k list.
+  uint32_t kc = kk;
+  int64_t tc = tk, cties = kties;
+  if (use_p) {
+    // masses of the top-k list; the ties at kk count only up to tk of them
+    __syncthreads();
+    for (int i = tid; i < 256; i += kThreads) sh.mass[i] = 0ull;
+    __syncthreads();
+    const bool partial_k = k < vocab && tk < kties;
+    const float wk = __expf(key_value(kk) * inv_t - xmax);
+    for_each_round<kVec>(p, vocab, [&](int64_t i0, const uint32_t* b) {
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        if (i0 + e >= vocab) break;
+        const uint32_t key = okey(b[e]);
+        if (key < kk || (partial_k && key == kk)) continue;
+        const float w = __expf(key_value(key) * inv_t - xmax);
+        atomicAdd(&sh.mass[key >> 8],
+                  static_cast<unsigned long long>(static_cast<double>(w) * kFix + 0.5));
+      }
+    });
+    __syncthreads();
+    unsigned long long wk_fix = static_cast<unsigned long long>(static_cast<double>(wk) * kFix + 0.5);
+    if (partial_k && tid == 0) sh.mass[kk >> 8] += wk_fix * static_cast<unsigned long long>(tk);
+    __syncthreads();
+    unsigned long long z = 0;
+    for (int i = 0; i < 256; ++i) z += sh.mass[i];
+    const double limit = static_cast<double>(pcut) * static_cast<double>(z);
+    // high byte of the cut: the bin holding the first position whose mass
+    // before it exceeds the limit
+    unsigned long long run = 0;
+    int hb = -1;
+    for (int bin = 255; bin >= 0; --bin) {
+      if (static_cast<double>(run + sh.mass[bin]) > limit) {
+        hb = bin;
+        break;
+      }
+      run += sh.mass[bin];
+    }
+    if (hb >= 0) {
+      const unsigned long long above_hi = run;
+      __syncthreads();
+      for (int i = tid; i < 256; i += kThreads) {
+        sh.mass[i] = 0ull;
+        sh.cnt[i] = 0;
+      }
+      __syncthreads();
+      for_each_round<kVec>(p, vocab, [&](int64_t i0, const uint32_t* b) {
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          if (i0 + e >= vocab) break;
+          const uint32_t key = okey(b[e]);
+          if (static_cast<int>(key >> 8) != hb || key < kk) continue;
+          atomicAdd(&sh.cnt[key & 0xFF], 1u);
+          if (partial_k && key == kk) continue;
+          const float w = __expf(key_value(key) * inv_t - xmax);
+          atomicAdd(&sh.mass[key & 0xFF],
+                    static_cast<unsigned long long>(static_cast<double>(w) * kFix + 0.5));
+        }
+      });
+      __syncthreads();
+      if (partial_k && static_cast<int>(kk >> 8) == hb && tid == 0) {
+        sh.mass[kk & 0xFF] += wk_fix * static_cast<unsigned long long>(tk);
+        sh.cnt[kk & 0xFF] = static_cast<uint32_t>(tk);
+      }
+      __syncthreads();
+      unsigned long long r2 = above_hi;
+      for (int bin = 255; bin >= 0; --bin) {
+        const unsigned long long m = sh.mass[bin];
+        if (sh.cnt[bin] == 0) continue;
+        if (static_cast<double>(r2 + m) > limit) {
+          // ties at this key: keep rank r while the mass before it, r2 +
+          // r * w, is within the limit (rank 0 of the list's first key is
+          // always kept since r2 is then 0)
+          const uint32_t key = (static_cast<uint32_t>(hb) << 8) | static_cast<uint32_t>(bin);
+          const unsigned long long w = m / sh.cnt[bin];
+          int64_t keep = 0;
+          while (keep < static_cast<int64_t>(sh.cnt[bin]) &&
+                 static_cast<double>(r2 + w * static_cast<unsigned long long>(keep)) <= limit)
+            ++keep;
+          if (keep == 0) keep = 1;  // cannot happen unless rounding: keep the first
+          // the top-p cut is inside the top-k list (its key >= kk)
+          kc = key;
+          cties = key == kk ? kties : sh.cnt[bin];
+          tc = key == kk ? (keep < tk ? keep : tk) : keep;
+          break;
+        }
+        r2 += m;
+      }
+    }
+  }
+
+  // ---- E: Gumbel-max over the kept tokens ---------------------------------
+  // kept: key > kc, or key == kc with tie rank < tc (no rank needed when all
+  // ties are kept, or when the cut is at a key nothing ties with)
+  const bool need_rank = tc < cties;
+  int64_t ties_before = 0;
+  unsigned long long bestk = 0;  // (ordered score, complemented index)
+  for_each_round<kVec>(p, vocab, [&](int64_t i0, const uint32_t* b) {
+    int rank0 = 0;
+    if (need_rank) {
+      int c = 0;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) c += (i0 + e < vocab && okey(b[e]) == kc) ? 1 : 0;
+      int total;
+      rank0 = block_scan_int(c, total, sh);
+      rank0 += static_cast<int>(ties_before);
+      ties_before += total;
+    }
+    int r = rank0;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      if (i0 + e >= vocab) break;
+      const uint32_t key = okey(b[e]);
+      bool kept = key > kc;
+      if (key == kc) {
+        kept = !need_rank || r < tc;
+        ++r;
+      }
+      if (!kept || key == 0) continue;
+      const float s = key_value(key) * inv_t + gumbel(seed, row, i0 + e);
+      const uint32_t sb = __float_as_uint(s);
+      const uint32_t so = (sb & 0x80000000u) ? ~sb : (sb | 0x80000000u);
+      const unsigned long long cand =
+          (static_cast<unsigned long long>(so) << 32) | (~static_cast<uint32_t>(i0 + e));
+      bestk = cand > bestk ? cand : bestk;
+    }
+  });
+#pragma unroll
+  for (int m = 1; m < 64; m <<= 1) {
+    const unsigned long long o = __shfl_xor(bestk, m, 64);
+    bestk = o > bestk ? o : bestk;
+  }
+  __syncthreads();
+  if (lane == 0) sh.best[wave] = bestk;
+  __syncthreads();
+  if (tid == 0) {
+    unsigned long long bb = 0;
+    for (int w = 0; w < kWaves; ++w) bb = sh.best[w] > bb ? sh.best[w] : bb;
+    out[row] = bb ? static_cast<int64_t>(~static_cast<uint32_t>(bb)) : 0;
+  }
+}
+
+}  // namespace
+
+extern "C" int qwen3_sample_bf16(const void* logits, int64_t row_stride, int64_t rows,
+                                 int64_t vocab, const float* temperature, const int32_t* top_k,
+                                 const float* top_p, uint64_t seed, int64_t* out, void* stream) {
+  const char* who = "qwen3_sample_bf16";
+  if (!logits || !out) return q3::fail(QWEN3_EINVAL, "%s: null pointer argument", who);
+  if (rows < 0 || rows > 0x7fffffff || vocab <= 0 || vocab > 0x7fffffff || row_stride < vocab)
+    return q3::fail(QWEN3_EINVAL, "%s: bad sizes", who);
+  if (rows == 0) return QWEN3_OK;
+  q3::clear_error();
+  auto s = static_cast<hipStream_t>(stream);
+  const auto lg = static_cast<const uint16_t*>(logits);
+  if (q3::aligned16(logits) && row_stride % 8 == 0)
+    hipLaunchKernelGGL(sample_kernel<true>, dim3(static_cast<unsigned>(rows)), dim3(kThreads), 0,
+                       s, lg, row_stride, vocab, temperature, top_k, top_p, seed, out);
+  else
+    hipLaunchKernelGGL(sample_kernel<false>, dim3(static_cast<unsigned>(rows)), dim3(kThreads), 0,
+                       s, lg, row_stride, vocab, temperature, top_k, top_p, seed, out);
+  return q3::launch_status(who);
+}

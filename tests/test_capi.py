@@ -155,6 +155,11 @@ def test_model_ops_reject_bad_arguments():
     assert lin(y=None) == -1
     assert lin(ss_in=FAKE, nw=None) == -1  # norm prologue without its weight
     assert lin(epi=2, N=1024) == -1        # silu: up half must start at or after row N
+    assert lib.qwen3_sample_bf16(FAKE, 100, 4, 151936, None, None, None, 1, FAKE, None) == -1
+    assert lib.qwen3_sample_bf16(None, 151936, 4, 151936, None, None, None, 1, FAKE, None) == -1
+    assert lib.qwen3_sample_bf16(FAKE, 151936, 0, 151936, None, None, None, 1, FAKE, None) == 0
+    assert lib.qwen3_page_in_bf16(FAKE, 8, 4, 16, FAKE, 2, FAKE, FAKE, 100, 10, None) == -1  # stride < pages
+    assert lib.qwen3_page_in_bf16(FAKE, 16, 4, 16, FAKE, 2, FAKE, FAKE, 100, 10, None) == -2  # odd block
     # nothing to do: no launch, success
     assert lib.qwen3_add_rms_norm_bf16(None, 0, FAKE, 1024, None, 0, FAKE, 1e-6, FAKE, 1024,
                                        None, 0, 0, 1024, None) == 0

@@ -460,3 +460,55 @@ def test_model_oracle_rejects_planted_mistakes(monkeypatch):
         with monkeypatch.context() as m:
             m.setattr(om, name, fn)
             assert err() > 1e-2, name
+
+
+# ---- sampling ----------------------------------------------------------------
+
+from oracle import sampling as osm  # noqa: E402
+
+
+def _reference_torch_keep(logits, temperature, top_k, top_p):
+    """The reference's own torch statement of the cut (qwen3/sampling.py:
+    76-102: topk, a mask of cumprobs > top_p shifted right by one), written
+    out independently of the oracle; returns the kept token set."""
+    x = torch.as_tensor(logits).double() / temperature
+    V = x.shape[0]
+    k = V if top_k <= 0 else min(top_k, V)
+    vals, idx = torch.sort(x, descending=True, stable=True)
+    vals, idx = vals[:k], idx[:k]
+    probs = torch.softmax(vals, -1)
+    remove = torch.cumsum(probs, -1) > top_p
+    remove[1:] = remove[:-1].clone()
+    remove[0] = False
+    return set(idx[~remove].tolist())
+
+
+@pytest.mark.parametrize("seed", range(6))
+def test_sampling_oracle_keep_rule_matches_reference_statement(seed):
+    g = torch.Generator().manual_seed(seed)
+    V = 300
+    logits = torch.randn(V, generator=g, dtype=torch.float64) * 3
+    for t, k, p in [(1.0, 0, 1.0), (0.7, 50, 0.9), (1.3, 0, 0.5), (1.0, 5, 1.0), (0.5, 400, 0.95)]:
+        assert osm.kept_set(logits, t, k, p) == _reference_torch_keep(logits, t, k, p), (t, k, p)
+
+
+def test_sampling_oracle_closed_forms():
+    logits = torch.tensor([1.0, 3.0, 2.0, 3.0, -1.0], dtype=torch.float64)
+    # greedy: first index of the maximum
+    assert osm.sampling_distribution(logits, 0.0).tolist() == [0, 1, 0, 0, 0]
+    # no truncation: the textbook softmax of logits / T
+    d = osm.sampling_distribution(logits, 2.0)
+    sm = torch.softmax(logits / 2.0, -1).numpy()
+    assert np.allclose(d, sm, atol=1e-15)
+    # top_k = 1 and a tiny top_p both collapse to the (first) argmax
+    assert osm.sampling_distribution(logits, 1.0, top_k=1)[1] == 1.0
+    assert osm.sampling_distribution(logits, 1.0, top_p=1e-9)[1] == 1.0
+    # ties at the top-k boundary keep the lower index
+    assert osm.kept_set(logits, 1.0, top_k=3) == {1, 3, 2}
+    assert osm.kept_set(torch.tensor([5.0, 4.0, 4.0, 4.0, 1.0]), 1.0, top_k=3) == {0, 1, 2}
+    # top-p keeps position j while the mass BEFORE it is <= p (an inclusive
+    # cumulative sum would drop the second token here)
+    two = torch.tensor([0.0, 0.0], dtype=torch.float64)
+    assert osm.kept_set(two, 1.0, top_p=0.5) == {0, 1}
+    inclusive = set(np.nonzero(np.cumsum([0.5, 0.5]) <= 0.5)[0].tolist())
+    assert inclusive != osm.kept_set(two, 1.0, top_p=0.5)
