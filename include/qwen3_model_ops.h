@@ -20,6 +20,11 @@
  *                              most 64 rows, with the RMSNorm before them, the
  *                              residual add after them or the SwiGLU activation
  *                              between them folded in
+ *   qwen3_decode_qkv_rope_bf16 <- input RMSNorm + qkv_proj + q_norm / k_norm +
+ *                              apply_rotary_pos_emb of a decode step
+ *                              (qwen3/decoder.py:47, attention.py:81-96) and the
+ *                              decode K/V write (update_kv_batch_triton,
+ *                              qwen3/kernels/paged_attention.py:353-377), one launch
  *   qwen3_embed_ss_bf16     <- the embedding lookup (qwen3/model.py:212) writing
  *                              the residual stream and its partial sums of squares
  *                              for the fused first norm
@@ -101,6 +106,33 @@ int qwen3_decode_linear_bf16(const void* x, int64_t x_row_stride,
                              const void* residual, int64_t residual_row_stride,
                              void* residual_out, int64_t residual_out_row_stride,
                              float* ss_out, int up_row, void* stream);
+
+/* Decode step of one layer up to attention, for M <= 64 tokens: with
+ * a = RMSNorm(h) (rms from ss_in as in qwen3_decode_linear_bf16), qkv =
+ * bf16(a @ qkv_weight^T) ((num_heads + 2 * num_kv_heads) * 128 rows: q heads,
+ * k heads, v heads), then per token exactly the decode form of
+ * qwen3_qk_norm_rope_decode_bf16: q and k heads RMS-normalised with their
+ * weights (head_eps) and rotated at positions[t] (NULL: seq_lens[row]); q
+ * stored to q_out (M, num_heads, 128), k and v written into the pool at
+ * position seq_lens[row] of row row_ids[t] (NULL: t) through the block
+ * table.  A position outside the tables gives a zero q row and no write.
+ * K a multiple of 64, at most 8192; head_dim 128. */
+int qwen3_decode_qkv_rope_bf16(const void* h, int64_t h_row_stride,
+                               const float* ss_in, int ss_in_tiles,
+                               const void* norm_weight, float eps,
+                               const void* qkv_weight, int64_t weight_row_stride,
+                               int M, int K, int num_heads, int num_kv_heads, int head_dim,
+                               const void* q_norm_weight, const void* k_norm_weight,
+                               float head_eps, const float* cos_table, const float* sin_table,
+                               int64_t table_row_stride, int64_t table_rows,
+                               const int64_t* positions,
+                               void* q_out, const int64_t q_out_strides[2],
+                               void* k_cache, const int64_t k_cache_strides[4],
+                               void* v_cache, const int64_t v_cache_strides[4],
+                               int64_t num_blocks, int layer_idx,
+                               const int32_t* seq_lens, const int32_t* block_table,
+                               int64_t bt_row_stride, int64_t max_rows, int64_t max_pages,
+                               const int32_t* row_ids, int block_size, void* stream);
 
 /* h_out[r] = embedding[ids[r]] (zero row for an id outside [0, vocab)) and
  * ss_out[r * (hidden / 16) + t] = sum of h^2 over columns 16t .. 16t + 15:

@@ -89,6 +89,13 @@ _SIGNATURES = {
          _vp, _i64, _vp, _i64, _vp, _i64, _vp, _i, _vp],
     ),
     "qwen3_embed_ss_bf16": (_i, [_vp, _vp, _i64, _i64, _i, _i, _vp, _i64, _vp, _vp]),
+    "qwen3_decode_qkv_rope_bf16": (
+        _i,
+        [_vp, _i64, _vp, _i, _vp, ctypes.c_float, _vp, _i64, _i, _i, _i, _i, _i,
+         _vp, _vp, ctypes.c_float, _vp, _vp, _i64, _i64, _vp,
+         _vp, _c_i64p, _vp, _c_i64p, _vp, _c_i64p, _i64, _i,
+         _vp, _vp, _i64, _i64, _i64, _vp, _i, _vp],
+    ),
 }
 
 ABI_VERSION = 3

@@ -15,7 +15,7 @@ import torch
 from .. import _lib
 
 __all__ = ["add_rms_norm", "embed_rms_norm", "silu_mul", "argmax", "advance_seq_lens",
-           "decode_linear", "embed_ss", "DECODE_LINEAR_MAX_ROWS"]
+           "decode_linear", "decode_qkv_rope", "embed_ss", "DECODE_LINEAR_MAX_ROWS"]
 
 DECODE_LINEAR_MAX_ROWS = 64
 _EPI = {"store": 0, "residual": 1, "silu": 2}
@@ -190,3 +190,42 @@ def embed_ss(ids: torch.Tensor, embed_weight: torch.Tensor, *, h_out: torch.Tens
                                          h_out.stride(0), ss_out.data_ptr(), _lib.stream_of(dev))
     _lib.check(rc, "qwen3_embed_ss_bf16")
     return h_out, ss_out
+
+
+def decode_qkv_rope(h: torch.Tensor, ss_in: torch.Tensor, norm_weight: torch.Tensor, eps: float,
+                    qkv_weight: torch.Tensor, num_heads: int, num_kv_heads: int,
+                    q_norm_weight: torch.Tensor, k_norm_weight: torch.Tensor, head_eps: float,
+                    cos_table: torch.Tensor, sin_table: torch.Tensor, pool, layer_idx: int,
+                    row_ids: torch.Tensor | None, positions: torch.Tensor | None = None,
+                    q_out: torch.Tensor | None = None) -> torch.Tensor:
+    """Input RMSNorm + qkv projection + QK-norm + RoPE + K/V pool write of a
+    decode step for at most 64 tokens in one launch; returns q (M, Hq, 128)
+    for the attention kernel (k and v go into `pool` at seq_lens[row])."""
+    h = _rows2d(h)
+    M, K = h.shape
+    D = 128
+    assert qkv_weight.shape == ((num_heads + 2 * num_kv_heads) * D, K)
+    assert ss_in.dtype == torch.float32 and ss_in.is_contiguous() and ss_in.shape[0] == M
+    assert cos_table.dtype == sin_table.dtype == torch.float32 and cos_table.stride(1) == 1
+    kb, vb = pool.k_buffer, pool.v_buffer
+    bt = pool.block_table_2d
+    dev = _lib.require_hip(h, ss_in, qkv_weight, kb, cos_table, row_ids)
+    if row_ids is not None:
+        assert row_ids.dtype == torch.int32 and row_ids.is_contiguous() and row_ids.numel() == M
+    if positions is not None:
+        positions = positions.reshape(-1)
+        assert positions.dtype == torch.int64 and positions.numel() == M
+        positions = positions.contiguous()
+    if q_out is None:
+        q_out = torch.empty(M, num_heads, D, dtype=h.dtype, device=h.device)
+    rc = _lib.load().qwen3_decode_qkv_rope_bf16(
+        h.data_ptr(), h.stride(0), ss_in.data_ptr(), ss_in.shape[1], norm_weight.data_ptr(),
+        float(eps), qkv_weight.data_ptr(), qkv_weight.stride(0), M, K, num_heads, num_kv_heads,
+        D, q_norm_weight.data_ptr(), k_norm_weight.data_ptr(), float(head_eps),
+        cos_table.data_ptr(), sin_table.data_ptr(), cos_table.stride(0), cos_table.shape[0],
+        _lib.ptr(positions), q_out.data_ptr(), _lib.strides(q_out, (0, 1)),
+        kb.data_ptr(), _lib.strides(kb, (0, 1, 2, 3)), vb.data_ptr(), _lib.strides(vb, (0, 1, 2, 3)),
+        kb.shape[0], int(layer_idx), pool.seq_lens.data_ptr(), bt.data_ptr(), bt.stride(0),
+        bt.shape[0], bt.shape[1], _lib.ptr(row_ids), kb.shape[3], _lib.stream_of(dev))
+    _lib.check(rc, "qwen3_decode_qkv_rope_bf16")
+    return q_out

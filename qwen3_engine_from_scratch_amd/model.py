@@ -34,7 +34,7 @@ import torch.nn.functional as F
 from .config import Qwen3Config
 from .kernels.flash_attention_varlen import flash_attention_prefill
 from .kernels.model_ops import (DECODE_LINEAR_MAX_ROWS, add_rms_norm, decode_linear,
-                                embed_rms_norm, embed_ss, silu_mul)
+                                decode_qkv_rope, embed_rms_norm, embed_ss, silu_mul)
 from .kernels.paged_attention import paged_attention_decode_hip, paged_decode_workspace_bytes
 from .kernels.pre_attention import qk_norm_rope_decode, qk_norm_rope_prefill, rope_tables
 
@@ -177,26 +177,34 @@ class Qwen3ForCausalLM(nn.Module):
         c = self.config
         widths = (c.hidden_size, c.num_attention_heads * c.head_dim, c.intermediate_size)
         return (batch <= DECODE_LINEAR_MAX_ROWS and all(w % 128 == 0 for w in widths)
-                and c.vocab_size % 16 == 0)
+                and c.head_dim == 128 and c.hidden_size <= 8192)
 
-    def _decode_fused(self, ids, attend) -> torch.Tensor:
-        """Decode step on the fused linears: the residual stream ping-pongs
+    def _decode_fused(self, ids, row_ids, pool, positions) -> torch.Tensor:
+        """Decode step on the fused kernels: the residual stream ping-pongs
         between two buffers, each with its per-16-column sums of squares, so
         every RMSNorm is the prologue of the linear after it and every
-        residual add the epilogue of the linear before it."""
+        residual add the epilogue of the linear before it; the qkv
+        projection also applies QK-norm and RoPE and writes K/V into the
+        pool, leaving one attention launch (plus its merge) per layer."""
         cfg = self.config
         eps = cfg.rms_norm_eps
         layers = self.model.layers
         B = ids.numel()
-        H, I = cfg.hidden_size, cfg.intermediate_size
+        Hq, Hkv, D = cfg.num_attention_heads, cfg.num_key_value_heads, cfg.head_dim
+        cos, sin = self.model.rotary_emb.tables(ids.device)
+        ws = self._workspace
         h_a, ss_a = embed_ss(ids, self.model.embed_tokens.weight)
         h_b = torch.empty_like(h_a)
         ss_b = torch.empty_like(ss_a)
         for i, layer in enumerate(layers):
             at = layer.self_attn
-            qkv = decode_linear(h_a, at.qkv_proj.weight, ss_in=ss_a,
-                                norm_weight=layer.input_layernorm.weight, eps=eps)
-            decode_linear(attend(i, at, qkv), at.o_proj.weight, epilogue="residual",
+            q = decode_qkv_rope(h_a, ss_a, layer.input_layernorm.weight, eps, at.qkv_proj.weight,
+                                Hq, Hkv, at.q_norm.weight, at.k_norm.weight, eps, cos, sin, pool,
+                                i, row_ids, positions)
+            o = paged_attention_decode_hip(q, pool.k_buffer[:, i], pool.v_buffer[:, i],
+                                           pool.block_table_2d, pool.seq_lens, row_ids,
+                                           pool.block_size, workspace=ws)
+            decode_linear(o.view(B, Hq * D), at.o_proj.weight, epilogue="residual",
                           residual=h_a, residual_out=h_b, ss_out=ss_b)
             act = decode_linear(h_b, layer.mlp.gate_up_proj.weight, epilogue="silu", ss_in=ss_b,
                                 norm_weight=layer.post_attention_layernorm.weight, eps=eps)
@@ -239,7 +247,10 @@ class Qwen3ForCausalLM(nn.Module):
         if fused is None:
             fused = self.fused_decode_ok(B)
         if fused:
-            return self._decode_fused(ids.reshape(-1).contiguous(), attend)
+            rows = row_ids if row_ids is not None else torch.arange(
+                B, dtype=torch.int32, device=ids.device)
+            return self._decode_fused(ids.reshape(-1).contiguous(), rows.contiguous(), pool,
+                                      positions)
         return self._run(ids.reshape(-1), attend, None)
 
     @torch.no_grad()

@@ -160,6 +160,16 @@ def test_model_ops_reject_bad_arguments():
     assert lib.qwen3_sample_bf16(FAKE, 151936, 0, 151936, None, None, None, 1, FAKE, None) == 0
     assert lib.qwen3_page_in_bf16(FAKE, 8, 4, 16, FAKE, 2, FAKE, FAKE, 100, 10, None) == -1  # stride < pages
     assert lib.qwen3_page_in_bf16(FAKE, 16, 4, 16, FAKE, 2, FAKE, FAKE, 100, 10, None) == -2  # odd block
+    s2, s4 = _s(2048, 128), _s(1 << 16, 1 << 14, 2048, 128)
+
+    def qkv(M=16, K=1024, D=128, ss=FAKE, bt_stride=8):
+        return lib.qwen3_decode_qkv_rope_bf16(
+            FAKE, K, ss, 64, FAKE, 1e-6, FAKE, K, M, K, 16, 8, D, FAKE, FAKE, 1e-6, FAKE, FAKE,
+            128, 64, None, FAKE, s2, FAKE, s4, FAKE, s4, 16, 0, FAKE, FAKE, bt_stride, 4, 8,
+            None, 16, None)
+
+    assert qkv(M=65) == -1 and qkv(D=64) == -3 and qkv(K=1000) == -3
+    assert qkv(ss=None) == -1 and qkv(bt_stride=4) == -1
     # nothing to do: no launch, success
     assert lib.qwen3_add_rms_norm_bf16(None, 0, FAKE, 1024, None, 0, FAKE, 1e-6, FAKE, 1024,
                                        None, 0, 0, 1024, None) == 0

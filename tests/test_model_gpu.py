@@ -215,6 +215,53 @@ def test_decode_linear_residual_and_silu_epilogues(gpu):
                                rtol=1e-5, atol=0)
 
 
+def test_decode_qkv_rope_vs_oracle(gpu):
+    """Input RMSNorm + qkv projection + QK-norm + RoPE + pool write in one
+    launch, against the oracle composition (fp32 projection rounded to bf16,
+    then the pre-attention oracle)."""
+    from oracle import pre_attention as opa
+    from qwen3_engine_from_scratch_amd.PagedKVcache import KVCachePool, PagedKVCache
+    from qwen3_engine_from_scratch_amd.kernels.model_ops import decode_qkv_rope
+
+    announce("decode qkv + QK-norm + RoPE + pool write")
+    g = torch.Generator().manual_seed(21)
+    M, K, Hq, Hkv = 37, 1024, 16, 8
+    h = (torch.randn(M, K, generator=g) * 2).to(torch.bfloat16)
+    wn = (1 + 0.1 * torch.randn(K, generator=g)).to(torch.bfloat16)
+    W = (torch.randn((Hq + 2 * Hkv) * 128, K, generator=g) * 0.03).to(torch.bfloat16)
+    qw = (1 + 0.1 * torch.randn(128, generator=g)).to(torch.bfloat16)
+    kw = (1 + 0.1 * torch.randn(128, generator=g)).to(torch.bfloat16)
+    ss = (h.float() ** 2).view(M, K // 16, 16).sum(-1).contiguous()
+    cos, sin = opa.rope_tables(128, 1e6, 2048)
+    pool = KVCachePool(4 * M + 8, 2, 16, Hkv, 128, device=gpu, dtype=torch.bfloat16,
+                       max_seq_len=1024, max_requests=M + 2)
+    caches = [PagedKVCache(pool) for _ in range(M)]
+    for c in caches:
+        c.seq_len = int(torch.randint(0, 40, (1,), generator=g))
+        while c.num_pages < c.seq_len // 16 + 1:
+            c._allocate_block()
+        pool.seq_lens[c.row_id] = c.seq_len
+    rows = torch.tensor([c.row_id for c in caches], dtype=torch.int32, device=gpu)
+    q = decode_qkv_rope(h.to(gpu), ss.to(gpu), wn.to(gpu), 1e-6, W.to(gpu), Hq, Hkv, qw.to(gpu),
+                        kw.to(gpu), 1e-6, cos.to(gpu), sin.to(gpu), pool, 1, rows)
+    torch.cuda.synchronize()
+    qkv = (oi.rms_norm(h, wn, 1e-6).float() @ W.float().T).to(torch.bfloat16)
+    qr = qkv[:, :Hq * 128].view(M, Hq, 128)
+    kr = qkv[:, Hq * 128:(Hq + Hkv) * 128].view(M, Hkv, 128)
+    vr = qkv[:, (Hq + Hkv) * 128:].view(M, Hkv, 128)
+    pos = torch.tensor([c.seq_len for c in caches])
+    q_ref, k_ref = opa.qk_norm_rope_ref(qr, kr, qw, kw, 1e-6, cos, sin, pos)
+    _close(q.reshape(M, -1), q_ref.reshape(M, -1), "q")
+    kb, vb = pool.k_buffer.cpu(), pool.v_buffer.cpu()
+    kp = torch.stack([kb[c.block_table[c.seq_len // 16], 1, :, c.seq_len % 16] for c in caches])
+    vp = torch.stack([vb[c.block_table[c.seq_len // 16], 1, :, c.seq_len % 16] for c in caches])
+    _close(kp.reshape(M, -1), k_ref.reshape(M, -1), "pool k")
+    _close(vp.reshape(M, -1), vr.reshape(M, -1), "pool v")
+    assert not kb[:, 0].any() and not vb[:, 0].any(), "other layers untouched"
+    written = sum(1 for _ in caches)
+    assert int((kb[:, 1].abs().sum(-1) > 0).sum()) == written * Hkv, "only the new slots written"
+
+
 def test_page_in_maps_and_zeroes_blocks(gpu):
     from qwen3_engine_from_scratch_amd.PagedKVcache import KVCachePool, PageIn, PagedKVCache
 
