@@ -45,7 +45,7 @@ constexpr int kWin = 64;       // block-table entries held per window (one per l
 constexpr int kStreamMaxB = 2048;       // batch entries tabulated in LDS
 constexpr int kStreamWgPerCu = 2;       // resident workgroups per CU (2 waves/SIMD)
 constexpr int kStreamMaxWgs = 1024;     // workspace sized for up to 512 CUs
-constexpr int kMinTilesPerWave = 16;
+constexpr int kMinTilesPerWave = 8;
 // Grid path (large batches).
 constexpr int kGridTilesPerWave = 32;
 constexpr int kGridTilesPerPart = kGridTilesPerWave * kWaves;
