@@ -116,7 +116,7 @@ int qwen3_decode_linear_bf16(const void* x, int64_t x_row_stride,
  * stored to q_out (M, num_heads, 128), k and v written into the pool at
  * position seq_lens[row] of row row_ids[t] (NULL: t) through the block
  * table.  A position outside the tables gives a zero q row and no write.
- * K a multiple of 64, at most 8192; head_dim 128. */
+ * K a multiple of 64, at most 4096; head_dim 128. */
 int qwen3_decode_qkv_rope_bf16(const void* h, int64_t h_row_stride,
                                const float* ss_in, int ss_in_tiles,
                                const void* norm_weight, float eps,

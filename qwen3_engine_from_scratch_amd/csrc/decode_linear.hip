@@ -127,6 +127,18 @@ __global__ __launch_bounds__(kWaves * 64) void decode_linear_kernel(LinArgs a) {
   Buf p, q;
   load(p, 0);
   load(q, kC);
+  // The residual this lane's outputs add to (wave 0 runs the epilogue),
+  // loaded now so its latency hides under the weight stream.
+  uint32_t res_pre[4] = {0u, 0u, 0u, 0u};
+  if constexpr (kEpi == kResidual) {
+    if (wave == 0) {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int row = rb * 16 + 4 * (lane >> 4) + i;
+        if (row < a.M) res_pre[i] = a.res[static_cast<int64_t>(row) * a.res_s + n0 + r16];
+      }
+    }
+  }
   if constexpr (kNorm) {
     for (int i = threadIdx.x; i < a.K / 8; i += kWaves * 64) nw_s[i] = q3::ld16(a.norm_w + 8 * i);
   }
@@ -221,8 +233,7 @@ __global__ __launch_bounds__(kWaves * 64) void decode_linear_kernel(LinArgs a) {
       float h = 0.f;
       if (live) {
         const float o = round_bf16(v[0][i]);
-        const float r = __uint_as_float(
-            static_cast<uint32_t>(a.res[static_cast<int64_t>(row) * a.res_s + col]) << 16);
+        const float r = __uint_as_float(res_pre[i] << 16);
         h = round_bf16(r + o);
         a.res_out[static_cast<int64_t>(row) * a.res_out_s + col] = to_bf16(h);
       }

@@ -12,9 +12,10 @@
 // waves are 8 column tiles of the head's 128 weight rows x 2 halves of K;
 // each streams 16 weight rows from HBM as the B operand of
 // mfma_f32_16x16x32_bf16 (loads coalesced per lane quad, redistributed with
-// ds_bpermute), with the RMSNorm of the residual stream h applied to the A
-// operand on the fly (rms from the producer's per-16-column partial sums of
-// h^2).  The head's 16 x 128 outputs meet in LDS, rounded to bf16 as the
+// ds_bpermute).  The A operand, the block's 16 rows of the residual stream h
+// after the input RMSNorm (rms from the producer's per-16-column partial
+// sums of h^2), is staged once in LDS by the whole workgroup and read from
+// there in the operand layout.  The head's 16 x 128 outputs meet in LDS, rounded to bf16 as the
 // projection's output is, and 16 lanes per token finish the head with the
 // arithmetic of the pre-attention kernel (same lane grouping, same
 // summation order, so the same bits).  The 16-token blocks of one head run
@@ -31,9 +32,9 @@ constexpr int kKParts = 2;
 constexpr int kWavesQ = kColTiles * kKParts;  // 16
 constexpr int kThreadsQ = kWavesQ * 64;       // 1024
 constexpr int kKStep = 32;
-constexpr int kC = 4;  // k-steps per prefetch buffer
+constexpr int kC = 8;  // k-steps per prefetch buffer (weights only)
 constexpr int kMaxRows = 64;
-constexpr int kMaxK = 8192;
+constexpr int kMaxK = 4096;  // staged A rows: 16 x (K + 8) bf16 in LDS
 constexpr int kXcds = 8;
 
 struct QkvArgs {
@@ -72,8 +73,9 @@ __device__ __forceinline__ float round_bf16(float x) {
 }
 
 __global__ __launch_bounds__(kThreadsQ) void qkv_rope_kernel(QkvArgs a) {
+  // The block's 16 normalised A rows, staged once: row r at a_s + r * pitch.
+  extern __shared__ uint16_t a_s[];
   __shared__ float rms_s[kRowsPerBlock];
-  __shared__ q3::u32x4 nw_s[kMaxK / 8];
   __shared__ float red[kColTiles][4][64];
   __shared__ uint16_t y_s[kRowsPerBlock][kD];
   __shared__ int64_t pos_s[kRowsPerBlock], phys_s[kRowsPerBlock];
@@ -97,15 +99,14 @@ __global__ __launch_bounds__(kThreadsQ) void qkv_rope_kernel(QkvArgs a) {
   const int kw = a.K / kKParts;
   const int k0 = kh * kw;
   const int steps = kw / kKStep;
+  const int pitch = a.K + 8;  // bf16 elements per staged row (16-byte pad: no bank conflicts)
 
-  // Coalesced loads (lane l: row l / 4, k-group l % 4) and the ds_bpermute
-  // that puts row L % 16, k-group L / 16 in lane L.
+  // Weights: coalesced loads (lane l: row l / 4, k-group l % 4) moved into
+  // the operand layout (lane L: row L % 16, k-group L / 16) by ds_bpermute.
   const int lrow = lane >> 2, lkg = 8 * (lane & 3);
   const int perm_addr = 4 * (4 * r16 + (lane >> 4));
   const uint16_t* wrow =
       a.w + static_cast<int64_t>(head * kD + ct * 16 + lrow) * a.w_s + lkg + k0;
-  const int xr = min(rb * 16 + lrow, a.M - 1);
-  const uint16_t* xrow = a.h + static_cast<int64_t>(xr) * a.h_s + lkg + k0;
   auto to_mfma = [&](q3::u32x4 v) {
     q3::u32x4 o;
 #pragma unroll
@@ -115,25 +116,35 @@ __global__ __launch_bounds__(kThreadsQ) void qkv_rope_kernel(QkvArgs a) {
   };
   struct Buf {
     q3::u32x4 b[kC];
-    q3::u32x4 x[kC];
   };
   auto load = [&](Buf& B, int s0) {
 #pragma unroll
     for (int u = 0; u < kC; ++u) {
       if (s0 + u >= steps) break;
-      const int k = (s0 + u) * kKStep;
-      B.b[u] = q3::ld16(wrow + k);
-      B.x[u] = q3::ld16(xrow + k);
+      B.b[u] = q3::ld16(wrow + (s0 + u) * kKStep);
     }
   };
   Buf p, q;
   load(p, 0);
   load(q, kC);
 
-  // Norm weight staged once; the rms of this block's rows; the position and
-  // pool slot of every token of the block (independent of the projection,
-  // so their loads overlap it).
-  for (int i = tid; i < a.K / 8; i += kThreadsQ) nw_s[i] = q3::ld16(a.norm_w + 8 * i);
+  // A rows and norm weight for this thread's first staging chunks (16 rows x
+  // K/8 chunks of 8), the rms of every row, and the position and pool slot
+  // of every token of the block: all independent of the weights, so their
+  // loads overlap them.
+  const int cpr = a.K >> 3;  // chunks per row
+  const int nchunks = kRowsPerBlock * cpr;
+  constexpr int kPre = 2;  // chunks per thread loaded early (all of them for K <= 1024)
+  q3::u32x4 hv[kPre], nv[kPre];
+  auto chunk_src = [&](int c, q3::u32x4& h, q3::u32x4& n) {
+    const int r = c / cpr, cc = c - r * cpr;
+    const int row = min(rb * 16 + r, a.M - 1);
+    h = q3::ld16(a.h + static_cast<int64_t>(row) * a.h_s + 8 * cc);
+    n = q3::ld16(a.norm_w + 8 * cc);
+  };
+#pragma unroll
+  for (int i = 0; i < kPre; ++i)
+    if (tid + i * kThreadsQ < nchunks) chunk_src(tid + i * kThreadsQ, hv[i], nv[i]);
   if (wave == 0) {
     const int row = min(rb * 16 + (lane >> 2), a.M - 1);
     const int part = lane & 3;
@@ -171,19 +182,35 @@ __global__ __launch_bounds__(kThreadsQ) void qkv_rope_kernel(QkvArgs a) {
     off_s[lane] = static_cast<int>(off);
   }
   __syncthreads();
-  const float rms = rms_s[r16];
+  // a = bf16((h * rms) * w), the input RMSNorm (qwen3/norm.py:22-26)
+  auto chunk_store = [&](int c, const q3::u32x4& h, const q3::u32x4& n) {
+    const int r = c / cpr, cc = c - r * cpr;
+    const float rr = rms_s[r];
+    q3::u32x4 o;
+#pragma unroll
+    for (int e = 0; e < 4; ++e)
+      o[e] = q3::pack_bf16x2((q3::bf16_lo(h[e]) * rr) * q3::bf16_lo(n[e]),
+                             (q3::bf16_hi(h[e]) * rr) * q3::bf16_hi(n[e]));
+    *reinterpret_cast<q3::u32x4*>(a_s + r * pitch + 8 * cc) = o;
+  };
+#pragma unroll
+  for (int i = 0; i < kPre; ++i)
+    if (tid + i * kThreadsQ < nchunks) chunk_store(tid + i * kThreadsQ, hv[i], nv[i]);
+  for (int c = tid + kPre * kThreadsQ; c < nchunks; c += kThreadsQ) {
+    q3::u32x4 h, n;
+    chunk_src(c, h, n);
+    chunk_store(c, h, n);
+  }
+  __syncthreads();
 
+  // A fragment of step s: lane L reads row L % 16, k = k0 + 32 s + 8 (L / 16).
+  const uint16_t* arow = a_s + r16 * pitch + k0 + kg;
   q3::f32x4 acc = {0.f, 0.f, 0.f, 0.f};
   auto compute = [&](const Buf& B, int s0) {
 #pragma unroll
     for (int u = 0; u < kC; ++u) {
       if (s0 + u >= steps) break;
-      q3::u32x4 av = to_mfma(B.x[u]);
-      const q3::u32x4 nw = nw_s[(k0 + kg + (s0 + u) * kKStep) >> 3];
-#pragma unroll
-      for (int e = 0; e < 4; ++e)
-        av[e] = q3::pack_bf16x2((q3::bf16_lo(av[e]) * rms) * q3::bf16_lo(nw[e]),
-                                (q3::bf16_hi(av[e]) * rms) * q3::bf16_hi(nw[e]));
+      const q3::u32x4 av = *reinterpret_cast<const q3::u32x4*>(arow + (s0 + u) * kKStep);
       acc = q3::mfma16x16x32(q3::as_bf16x8(av), q3::as_bf16x8(to_mfma(B.b[u])), acc);
     }
   };
@@ -377,7 +404,8 @@ extern "C" int qwen3_decode_qkv_rope_bf16(
   const int heads = num_heads + 2 * num_kv_heads;
   const int64_t blocks = q3::cdiv(heads, kXcds) * kXcds * ((M + 15) / 16);
   q3::clear_error();
-  hipLaunchKernelGGL(qkv_rope_kernel, dim3(static_cast<unsigned>(blocks)), dim3(kThreadsQ), 0,
+  const size_t lds = static_cast<size_t>(kRowsPerBlock) * (K + 8) * sizeof(uint16_t);
+  hipLaunchKernelGGL(qkv_rope_kernel, dim3(static_cast<unsigned>(blocks)), dim3(kThreadsQ), lds,
                      static_cast<hipStream_t>(stream), a);
   return q3::launch_status(who);
 }

@@ -177,7 +177,7 @@ class Qwen3ForCausalLM(nn.Module):
         c = self.config
         widths = (c.hidden_size, c.num_attention_heads * c.head_dim, c.intermediate_size)
         return (batch <= DECODE_LINEAR_MAX_ROWS and all(w % 128 == 0 for w in widths)
-                and c.head_dim == 128 and c.hidden_size <= 8192)
+                and c.head_dim == 128 and c.hidden_size <= 4096)
 
     def _decode_fused(self, ids, row_ids, pool, positions) -> torch.Tensor:
         """Decode step on the fused kernels: the residual stream ping-pongs

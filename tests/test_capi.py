@@ -168,7 +168,7 @@ def test_model_ops_reject_bad_arguments():
             128, 64, None, FAKE, s2, FAKE, s4, FAKE, s4, 16, 0, FAKE, FAKE, bt_stride, 4, 8,
             None, 16, None)
 
-    assert qkv(M=65) == -1 and qkv(D=64) == -3 and qkv(K=1000) == -3
+    assert qkv(M=65) == -1 and qkv(D=64) == -3 and qkv(K=1000) == -3 and qkv(K=4160) == -3
     assert qkv(ss=None) == -1 and qkv(bt_stride=4) == -1
     # nothing to do: no launch, success
     assert lib.qwen3_add_rms_norm_bf16(None, 0, FAKE, 1024, None, 0, FAKE, 1e-6, FAKE, 1024,

@@ -215,7 +215,8 @@ def test_decode_linear_residual_and_silu_epilogues(gpu):
                                rtol=1e-5, atol=0)
 
 
-def test_decode_qkv_rope_vs_oracle(gpu):
+@pytest.mark.parametrize("M,K", [(37, 1024), (64, 4096), (5, 2048)])
+def test_decode_qkv_rope_vs_oracle(gpu, M, K):
     """Input RMSNorm + qkv projection + QK-norm + RoPE + pool write in one
     launch, against the oracle composition (fp32 projection rounded to bf16,
     then the pre-attention oracle)."""
@@ -223,9 +224,9 @@ def test_decode_qkv_rope_vs_oracle(gpu):
     from qwen3_engine_from_scratch_amd.PagedKVcache import KVCachePool, PagedKVCache
     from qwen3_engine_from_scratch_amd.kernels.model_ops import decode_qkv_rope
 
-    announce("decode qkv + QK-norm + RoPE + pool write")
-    g = torch.Generator().manual_seed(21)
-    M, K, Hq, Hkv = 37, 1024, 16, 8
+    announce(f"decode qkv + QK-norm + RoPE + pool write M={M} K={K}")
+    g = torch.Generator().manual_seed(21 + K + M)
+    Hq, Hkv = 16, 8
     h = (torch.randn(M, K, generator=g) * 2).to(torch.bfloat16)
     wn = (1 + 0.1 * torch.randn(K, generator=g)).to(torch.bfloat16)
     W = (torch.randn((Hq + 2 * Hkv) * 128, K, generator=g) * 0.03).to(torch.bfloat16)
