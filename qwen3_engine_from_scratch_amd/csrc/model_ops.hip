@@ -161,14 +161,26 @@ __global__ __launch_bounds__(kArgmaxThreads) void argmax_kernel(const uint16_t* 
   const uint16_t* p = logits + row * row_s;
   uint64_t best = 0;  // below every real key
   if constexpr (kVec) {
+    // eight 16-byte loads in flight per thread before any is used
+    constexpr int kBatch = 8;
     const int64_t nvec = vocab >> 3;
-    for (int64_t c = threadIdx.x; c < nvec; c += kArgmaxThreads) {
-      const q3::u32x4 v = q3::ld16(p + 8 * c);
-      const uint32_t base = static_cast<uint32_t>(8 * c);
+    for (int64_t c0 = threadIdx.x; c0 < nvec; c0 += kArgmaxThreads * kBatch) {
+      q3::u32x4 v[kBatch];
 #pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        best = umax64(best, argmax_key(v[e] & 0xFFFFu, base + 2 * e));
-        best = umax64(best, argmax_key(v[e] >> 16, base + 2 * e + 1));
+      for (int u = 0; u < kBatch; ++u) {
+        const int64_t c = c0 + u * kArgmaxThreads;
+        if (c < nvec) v[u] = q3::ld16(p + 8 * c);
+      }
+#pragma unroll
+      for (int u = 0; u < kBatch; ++u) {
+        const int64_t c = c0 + u * kArgmaxThreads;
+        if (c >= nvec) break;
+        const uint32_t base = static_cast<uint32_t>(8 * c);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          best = umax64(best, argmax_key(v[u][e] & 0xFFFFu, base + 2 * e));
+          best = umax64(best, argmax_key(v[u][e] >> 16, base + 2 * e + 1));
+        }
       }
     }
   } else {

@@ -11,19 +11,23 @@
 //                        restricted to them.
 // Ties in value are ordered by token index (lower first).  The random
 // stream is this file's own (Philox4x32-10 keyed by seed and row, counter =
-// token index), so draws are reproducible for a seed but are not the
-// reference's stream; the distribution is the same.
+// token index / 4, one 32-bit draw per token), so draws are reproducible for
+// a seed but are not the reference's stream; the distribution is the same.
 //
 // One 1024-thread workgroup per row, passes over the row (L2-resident after
 // the first):
-//   A  count histogram of the high byte of the 16-bit order-preserving key,
-//      and the maximum key
-//   B  count histogram of the low byte inside the top-k boundary bin -> the
-//      exact k-th largest key and how many of its ties are kept
-//   C  softmax mass histogram (high byte) of the top-k set, and its total
-//   D  low-byte mass histogram inside the top-p boundary bin -> the exact
+//   A  count histogram of the high 12 bits of the 16-bit order-preserving
+//      key, and the maximum key
+//   B  count histogram of the low 4 bits inside the top-k boundary bin ->
+//      the exact k-th largest key and how many of its ties are kept
+//   C  softmax mass histogram (high 12 bits) of the top-k set, and its total
+//   D  low-4-bit mass histogram inside the top-p boundary bin -> the exact
 //      top-p cut
 //   E  Gumbel-max over the kept tokens
+// 4096 high bins keep the LDS atomics of a wave mostly on distinct
+// addresses (logits crowd into a few binades: 256 bins of sign + exponent
+// would serialise them), and the boundary bins are found by a block-wide
+// scan over four bins per thread.
 // Masses are summed as 64-bit fixed point (2^40 per unit), so every
 // histogram and the cut are independent of summation order.
 #include "common.hpp"
@@ -53,8 +57,8 @@ __device__ __forceinline__ uint32_t mulhilo(uint32_t a, uint32_t b, uint32_t& hi
   hi = static_cast<uint32_t>(p >> 32);
   return static_cast<uint32_t>(p);
 }
-__device__ __forceinline__ uint32_t philox_first(uint32_t c0, uint32_t c1, uint32_t c2,
-                                                 uint32_t c3, uint32_t k0, uint32_t k1) {
+__device__ __forceinline__ q3::u32x4 philox4(uint32_t c0, uint32_t c1, uint32_t c2, uint32_t c3,
+                                              uint32_t k0, uint32_t k1) {
 #pragma unroll
   for (int r = 0; r < 10; ++r) {
     uint32_t hi0, hi1;
@@ -65,24 +69,37 @@ __device__ __forceinline__ uint32_t philox_first(uint32_t c0, uint32_t c1, uint3
     k0 += 0x9E3779B9u;
     k1 += 0xBB67AE85u;
   }
-  return c0;
+  return q3::u32x4{c0, c1, c2, c3};
 }
-// Standard Gumbel noise of token i of a row: u in (0, 1), g = -log(-log u).
-__device__ __forceinline__ float gumbel(uint64_t seed, int64_t row, int64_t i) {
-  const uint32_t r = philox_first(static_cast<uint32_t>(i), static_cast<uint32_t>(i >> 32),
-                                  static_cast<uint32_t>(row), 0x5EED5EEDu,
-                                  static_cast<uint32_t>(seed), static_cast<uint32_t>(seed >> 32));
+// The four 32-bit draws of tokens 4n .. 4n+3 of a row: one Philox block,
+// counter (n, row, constant), key = seed.
+__device__ __forceinline__ q3::u32x4 draws4(uint64_t seed, int64_t row, int64_t n) {
+  return philox4(static_cast<uint32_t>(n), static_cast<uint32_t>(n >> 32),
+                 static_cast<uint32_t>(row), 0x5EED5EEDu, static_cast<uint32_t>(seed),
+                 static_cast<uint32_t>(seed >> 32));
+}
+// Standard Gumbel noise of a 32-bit draw: u in (0, 1), g = -log(-log u).
+__device__ __forceinline__ float gumbel_of(uint32_t r) {
   const float u = (static_cast<float>(r >> 8) + 0.5f) * (1.f / 16777216.f);
-  return -logf(-logf(u));
+  return -__logf(-__logf(u));
 }
 
+constexpr int kLoBits = 4;
+constexpr int kLoBins = 1 << kLoBits;              // 16
+constexpr int kHiBins = 1 << (16 - kLoBits);       // 4096
+constexpr int kBinsPerThread = kHiBins / kThreads;  // 4
+
 struct Shared {
-  uint32_t cnt[256];
-  unsigned long long mass[256];
+  uint32_t cnt[kHiBins];
+  unsigned long long mass[kHiBins];
+  uint32_t lo_cnt[kLoBins];
+  unsigned long long lo_mass[kLoBins];
   int wsum[kWaves];
   unsigned long long wmass[kWaves];
   uint32_t wmax[kWaves];
   unsigned long long best[kWaves];
+  int sel_bin;
+  unsigned long long sel_run;
 };
 
 // Block-wide sums; every thread gets the result.
@@ -121,35 +138,75 @@ __device__ __forceinline__ int block_scan_int(int v, int& total, Shared& sh) {
   return before + incl - v;
 }
 
+// The same scan over 64-bit values.
+__device__ __forceinline__ unsigned long long block_scan_u64(unsigned long long v,
+                                                             unsigned long long& total,
+                                                             Shared& sh) {
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  unsigned long long incl = v;
+#pragma unroll
+  for (int o = 1; o < 64; o <<= 1) {
+    const unsigned long long y = __shfl_up(incl, o, 64);
+    if (lane >= o) incl += y;
+  }
+  __syncthreads();
+  if (lane == 63) sh.wmass[wave] = incl;
+  __syncthreads();
+  unsigned long long before = 0;
+  total = 0;
+#pragma unroll
+  for (int w = 0; w < kWaves; ++w) {
+    if (w < wave) before += sh.wmass[w];
+    total += sh.wmass[w];
+  }
+  return before + incl - v;
+}
+
 // Visits the row in rounds of kThreads * 8 tokens: thread t gets tokens
-// base + 8t .. base + 8t + 7 of each round (16-byte loads when aligned).
+// base + 8t .. base + 8t + 7 of each round (16-byte loads when aligned).  The
+// loads of kBatch rounds are issued before any is used, so a pass over the
+// row waits for memory once per batch rather than once per round.
 template <bool kVec, typename F>
 __device__ __forceinline__ void for_each_round(const uint16_t* p, int64_t vocab, F&& f) {
+  constexpr int kBatch = kVec ? 8 : 2;  // element loads hold more registers
   const int64_t per_round = static_cast<int64_t>(kThreads) * 8;
-  for (int64_t base = 0; base < vocab; base += per_round) {
-    const int64_t i0 = base + 8 * static_cast<int64_t>(threadIdx.x);
-    uint32_t b[8];
-    if (kVec && i0 + 8 <= vocab) {
-      const q3::u32x4 v = q3::ld16(p + i0);
+  for (int64_t base = 0; base < vocab; base += per_round * kBatch) {
+    q3::u32x4 v[kBatch];
+#pragma unroll
+    for (int u = 0; u < kBatch; ++u) {
+      const int64_t i0 = base + u * per_round + 8 * static_cast<int64_t>(threadIdx.x);
+      if (kVec && i0 + 8 <= vocab) {
+        v[u] = q3::ld16(p + i0);
+      } else {
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const uint32_t lo = i0 + 2 * e < vocab ? p[i0 + 2 * e] : 0x7FC1u;  // NaN pad
+          const uint32_t hi = i0 + 2 * e + 1 < vocab ? p[i0 + 2 * e + 1] : 0x7FC1u;
+          v[u][e] = lo | (hi << 16);
+        }
+      }
+    }
+#pragma unroll
+    for (int u = 0; u < kBatch; ++u) {
+      const int64_t i0 = base + u * per_round + 8 * static_cast<int64_t>(threadIdx.x);
+      if (base + u * per_round >= vocab) break;  // uniform: the round is past the row
+      uint32_t b[8];
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
-        b[2 * e] = v[e] & 0xFFFFu;
-        b[2 * e + 1] = v[e] >> 16;
+        b[2 * e] = v[u][e] & 0xFFFFu;
+        b[2 * e + 1] = v[u][e] >> 16;
       }
-    } else {
-#pragma unroll
-      for (int e = 0; e < 8; ++e) b[e] = i0 + e < vocab ? p[i0 + e] : 0x7FC1u;  // NaN pad
+      f(i0, b);
     }
-    f(i0, b);
   }
 }
 
-// Scans a 256-bin count histogram from the top: returns the bin where the
+// Scans the low-bit count histogram from the top: returns the bin where the
 // running count (starting at `above`) first reaches `need`, and the count
 // strictly above that bin.
 __device__ __forceinline__ int find_count_bin(const uint32_t* h, int64_t need, int64_t& above) {
   int64_t run = above;
-  for (int bin = 255; bin >= 0; --bin) {
+  for (int bin = kLoBins - 1; bin >= 0; --bin) {
     if (run + h[bin] >= need) {
       above = run;
       return bin;
@@ -158,6 +215,69 @@ __device__ __forceinline__ int find_count_bin(const uint32_t* h, int64_t need, i
   }
   above = run;
   return 0;
+}
+
+// The same over the 4096 high bins, by the whole block: thread t sums bins
+// 4095 - 4t .. 4092 - 4t, an exclusive scan gives the count above them, and
+// the one thread whose range holds the crossing walks its four bins.  Every
+// thread returns the bin and sets `above`; the histogram must hold at least
+// `need` counts.
+__device__ __forceinline__ int find_count_bin_block(const uint32_t* h, int64_t need,
+                                                    int64_t& above, Shared& sh) {
+  const int top = kHiBins - 1 - kBinsPerThread * static_cast<int>(threadIdx.x);
+  int mine = 0;
+#pragma unroll
+  for (int j = 0; j < kBinsPerThread; ++j) mine += static_cast<int>(h[top - j]);
+  int total;
+  const int before = block_scan_int(mine, total, sh);
+  int64_t run = before;
+  if (run < need && need <= run + mine) {
+#pragma unroll
+    for (int j = 0; j < kBinsPerThread; ++j) {
+      if (run + h[top - j] >= need) {
+        sh.sel_bin = top - j;
+        sh.sel_run = static_cast<unsigned long long>(run);
+        break;
+      }
+      run += h[top - j];
+    }
+  }
+  __syncthreads();
+  above = static_cast<int64_t>(sh.sel_run);
+  return sh.sel_bin;
+}
+
+// The top-p boundary over the 4096 high mass bins: limit = top_p x total
+// (top_p clamped at 0), and the first bin from the top whose inclusive mass,
+// converted to double, exceeds it (there is one when top_p < 1 and the total
+// is positive).  Returns the bin, or -1, and sets `run` to the mass above
+// it.  The same block-wide scan as find_count_bin_block; the caller has
+// passed a barrier since the last read of sh.sel_bin.
+__device__ __forceinline__ int find_mass_bin_block(const unsigned long long* m, float top_p,
+                                                   double& limit, unsigned long long& run,
+                                                   Shared& sh) {
+  const int top = kHiBins - 1 - kBinsPerThread * static_cast<int>(threadIdx.x);
+  unsigned long long mine = 0;
+#pragma unroll
+  for (int j = 0; j < kBinsPerThread; ++j) mine += m[top - j];
+  if (threadIdx.x == 0) sh.sel_bin = -1;  // before the scan's barriers
+  unsigned long long total;
+  unsigned long long r = block_scan_u64(mine, total, sh);
+  limit = static_cast<double>(fmaxf(top_p, 0.f)) * static_cast<double>(total);
+  if (static_cast<double>(r) <= limit && static_cast<double>(r + mine) > limit) {
+#pragma unroll
+    for (int j = 0; j < kBinsPerThread; ++j) {
+      if (static_cast<double>(r + m[top - j]) > limit) {
+        sh.sel_bin = top - j;
+        sh.sel_run = r;
+        break;
+      }
+      r += m[top - j];
+    }
+  }
+  __syncthreads();
+  run = sh.sel_run;
+  return sh.sel_bin;
 }
 
 template <bool kVec>
@@ -210,8 +330,9 @@ __global__ __launch_bounds__(kThreads) void sample_kernel(const uint16_t* logits
   const bool use_p = pcut < 1.f;
   const float inv_t = 1.f / temp;
 
-  // ---- A: high-byte counts and the maximum key --------------------------
-  for (int i = tid; i < 256; i += kThreads) sh.cnt[i] = 0;
+  // ---- A: high-bin counts and the maximum key ----------------------------
+  for (int i = tid; i < kHiBins; i += kThreads) sh.cnt[i] = 0;
+  if (tid < kLoBins) sh.lo_cnt[tid] = 0;
   __syncthreads();
   uint32_t kmax = 0;
   for_each_round<kVec>(p, vocab, [&](int64_t i0, const uint32_t* b) {
@@ -220,7 +341,7 @@ __global__ __launch_bounds__(kThreads) void sample_kernel(const uint16_t* logits
       if (i0 + e >= vocab) break;
       const uint32_t key = okey(b[e]);
       kmax = key > kmax ? key : kmax;
-      atomicAdd(&sh.cnt[key >> 8], 1u);
+      atomicAdd(&sh.cnt[key >> kLoBits], 1u);
     }
   });
 #pragma unroll
@@ -240,22 +361,19 @@ __global__ __launch_bounds__(kThreads) void sample_kernel(const uint16_t* logits
   int64_t tk = 0, kties = 0;
   if (k < vocab) {
     int64_t above = 0;
-    const int hb = find_count_bin(sh.cnt, k, above);
-    __syncthreads();
-    for (int i = tid; i < 256; i += kThreads) sh.cnt[i] = 0;
-    __syncthreads();
+    const int hb = find_count_bin_block(sh.cnt, k, above, sh);
     for_each_round<kVec>(p, vocab, [&](int64_t i0, const uint32_t* b) {
 #pragma unroll
       for (int e = 0; e < 8; ++e) {
         if (i0 + e >= vocab) break;
         const uint32_t key = okey(b[e]);
-        if (static_cast<int>(key >> 8) == hb) atomicAdd(&sh.cnt[key & 0xFF], 1u);
+        if (static_cast<int>(key >> kLoBits) == hb) atomicAdd(&sh.lo_cnt[key & (kLoBins - 1)], 1u);
       }
     });
     __syncthreads();
-    const int lb = find_count_bin(sh.cnt, k, above);
-    kk = (static_cast<uint32_t>(hb) << 8) | static_cast<uint32_t>(lb);
-    kties = sh.cnt[lb];
+    const int lb = find_count_bin(sh.lo_cnt, k, above);
+    kk = (static_cast<uint32_t>(hb) << kLoBits) | static_cast<uint32_t>(lb);
+    kties = sh.lo_cnt[lb];
     tk = k - above;  // 1 <= tk <= kties
   }
   // membership in the top-k list before tie ranks: key > kk, or key == kk
@@ -269,7 +387,11 @@ __global__ __launch_bounds__(kThreads) void sample_kernel(const uint16_t* logits
   if (use_p) {
     // masses of the top-k list; the ties at kk count only up to tk of them
     __syncthreads();
-    for (int i = tid; i < 256; i += kThreads) sh.mass[i] = 0ull;
+    for (int i = tid; i < kHiBins; i += kThreads) sh.mass[i] = 0ull;
+    if (tid < kLoBins) {
+      sh.lo_mass[tid] = 0ull;
+      sh.lo_cnt[tid] = 0;
+    }
     __syncthreads();
     const bool partial_k = k < vocab && tk < kties;
     const float wk = __expf(key_value(kk) * inv_t - xmax);
@@ -280,78 +402,63 @@ __global__ __launch_bounds__(kThreads) void sample_kernel(const uint16_t* logits
         const uint32_t key = okey(b[e]);
         if (key < kk || (partial_k && key == kk)) continue;
         const float w = __expf(key_value(key) * inv_t - xmax);
-        atomicAdd(&sh.mass[key >> 8],
+        atomicAdd(&sh.mass[key >> kLoBits],
                   static_cast<unsigned long long>(static_cast<double>(w) * kFix + 0.5));
       }
     });
     __syncthreads();
-    unsigned long long wk_fix = static_cast<unsigned long long>(static_cast<double>(wk) * kFix + 0.5);
-    if (partial_k && tid == 0) sh.mass[kk >> 8] += wk_fix * static_cast<unsigned long long>(tk);
+    const unsigned long long wk_fix =
+        static_cast<unsigned long long>(static_cast<double>(wk) * kFix + 0.5);
+    if (partial_k && tid == 0) sh.mass[kk >> kLoBits] += wk_fix * static_cast<unsigned long long>(tk);
     __syncthreads();
-    unsigned long long z = 0;
-    for (int i = 0; i < 256; ++i) z += sh.mass[i];
-    const double limit = static_cast<double>(pcut) * static_cast<double>(z);
-    // high byte of the cut: the bin holding the first position whose mass
+    // high bins of the cut: the bin holding the first position whose mass
     // before it exceeds the limit
-    unsigned long long run = 0;
-    int hb = -1;
-    for (int bin = 255; bin >= 0; --bin) {
-      if (static_cast<double>(run + sh.mass[bin]) > limit) {
-        hb = bin;
+    double limit;
+    unsigned long long above_hi;
+    const int hb = find_mass_bin_block(sh.mass, pcut, limit, above_hi, sh);
+    if (hb >= 0) {  // else a row without mass (all NaN): no cut
+    for_each_round<kVec>(p, vocab, [&](int64_t i0, const uint32_t* b) {
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        if (i0 + e >= vocab) break;
+        const uint32_t key = okey(b[e]);
+        if (static_cast<int>(key >> kLoBits) != hb || key < kk) continue;
+        atomicAdd(&sh.lo_cnt[key & (kLoBins - 1)], 1u);
+        if (partial_k && key == kk) continue;
+        const float w = __expf(key_value(key) * inv_t - xmax);
+        atomicAdd(&sh.lo_mass[key & (kLoBins - 1)],
+                  static_cast<unsigned long long>(static_cast<double>(w) * kFix + 0.5));
+      }
+    });
+    __syncthreads();
+    if (partial_k && static_cast<int>(kk >> kLoBits) == hb && tid == 0) {
+      sh.lo_mass[kk & (kLoBins - 1)] += wk_fix * static_cast<unsigned long long>(tk);
+      sh.lo_cnt[kk & (kLoBins - 1)] = static_cast<uint32_t>(tk);
+    }
+    __syncthreads();
+    unsigned long long r2 = above_hi;
+    for (int bin = kLoBins - 1; bin >= 0; --bin) {
+      const unsigned long long m = sh.lo_mass[bin];
+      if (sh.lo_cnt[bin] == 0) continue;
+      if (static_cast<double>(r2 + m) > limit) {
+        // ties at this key: keep rank r while the mass before it, r2 +
+        // r * w, is within the limit (rank 0 of the list's first key is
+        // always kept since r2 is then 0)
+        const uint32_t key = (static_cast<uint32_t>(hb) << kLoBits) | static_cast<uint32_t>(bin);
+        const unsigned long long w = m / sh.lo_cnt[bin];
+        int64_t keep = 0;
+        while (keep < static_cast<int64_t>(sh.lo_cnt[bin]) &&
+               static_cast<double>(r2 + w * static_cast<unsigned long long>(keep)) <= limit)
+          ++keep;
+        if (keep == 0) keep = 1;  // cannot happen unless rounding: keep the first
+        // the top-p cut is inside the top-k list (its key >= kk)
+        kc = key;
+        cties = key == kk ? kties : sh.lo_cnt[bin];
+        tc = key == kk ? (keep < tk ? keep : tk) : keep;
         break;
       }
-      run += sh.mass[bin];
+      r2 += m;
     }
-    if (hb >= 0) {
-      const unsigned long long above_hi = run;
-      __syncthreads();
-      for (int i = tid; i < 256; i += kThreads) {
-        sh.mass[i] = 0ull;
-        sh.cnt[i] = 0;
-      }
-      __syncthreads();
-      for_each_round<kVec>(p, vocab, [&](int64_t i0, const uint32_t* b) {
-#pragma unroll
-        for (int e = 0; e < 8; ++e) {
-          if (i0 + e >= vocab) break;
-          const uint32_t key = okey(b[e]);
-          if (static_cast<int>(key >> 8) != hb || key < kk) continue;
-          atomicAdd(&sh.cnt[key & 0xFF], 1u);
-          if (partial_k && key == kk) continue;
-          const float w = __expf(key_value(key) * inv_t - xmax);
-          atomicAdd(&sh.mass[key & 0xFF],
-                    static_cast<unsigned long long>(static_cast<double>(w) * kFix + 0.5));
-        }
-      });
-      __syncthreads();
-      if (partial_k && static_cast<int>(kk >> 8) == hb && tid == 0) {
-        sh.mass[kk & 0xFF] += wk_fix * static_cast<unsigned long long>(tk);
-        sh.cnt[kk & 0xFF] = static_cast<uint32_t>(tk);
-      }
-      __syncthreads();
-      unsigned long long r2 = above_hi;
-      for (int bin = 255; bin >= 0; --bin) {
-        const unsigned long long m = sh.mass[bin];
-        if (sh.cnt[bin] == 0) continue;
-        if (static_cast<double>(r2 + m) > limit) {
-          // ties at this key: keep rank r while the mass before it, r2 +
-          // r * w, is within the limit (rank 0 of the list's first key is
-          // always kept since r2 is then 0)
-          const uint32_t key = (static_cast<uint32_t>(hb) << 8) | static_cast<uint32_t>(bin);
-          const unsigned long long w = m / sh.cnt[bin];
-          int64_t keep = 0;
-          while (keep < static_cast<int64_t>(sh.cnt[bin]) &&
-                 static_cast<double>(r2 + w * static_cast<unsigned long long>(keep)) <= limit)
-            ++keep;
-          if (keep == 0) keep = 1;  // cannot happen unless rounding: keep the first
-          // the top-p cut is inside the top-k list (its key >= kk)
-          kc = key;
-          cties = key == kk ? kties : sh.cnt[bin];
-          tc = key == kk ? (keep < tk ? keep : tk) : keep;
-          break;
-        }
-        r2 += m;
-      }
     }
   }
 
@@ -373,22 +480,33 @@ __global__ __launch_bounds__(kThreads) void sample_kernel(const uint16_t* logits
       ties_before += total;
     }
     int r = rank0;
+    bool kept[8];
 #pragma unroll
     for (int e = 0; e < 8; ++e) {
-      if (i0 + e >= vocab) break;
       const uint32_t key = okey(b[e]);
-      bool kept = key > kc;
-      if (key == kc) {
-        kept = !need_rank || r < tc;
+      bool kp = key > kc;
+      if (key == kc && i0 + e < vocab) {
+        kp = !need_rank || r < tc;
         ++r;
       }
-      if (!kept || key == 0) continue;
-      const float s = key_value(key) * inv_t + gumbel(seed, row, i0 + e);
-      const uint32_t sb = __float_as_uint(s);
-      const uint32_t so = (sb & 0x80000000u) ? ~sb : (sb | 0x80000000u);
-      const unsigned long long cand =
-          (static_cast<unsigned long long>(so) << 32) | (~static_cast<uint32_t>(i0 + e));
-      bestk = cand > bestk ? cand : bestk;
+      kept[e] = kp && key != 0 && i0 + e < vocab;
+    }
+    // one Philox block per four tokens (i0 is a multiple of 8)
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      if (!(kept[4 * h] || kept[4 * h + 1] || kept[4 * h + 2] || kept[4 * h + 3])) continue;
+      const q3::u32x4 d = draws4(seed, row, (i0 >> 2) + h);
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const int e = 4 * h + j;
+        if (!kept[e]) continue;
+        const float sc = key_value(okey(b[e])) * inv_t + gumbel_of(d[j]);
+        const uint32_t sb = __float_as_uint(sc);
+        const uint32_t so = (sb & 0x80000000u) ? ~sb : (sb | 0x80000000u);
+        const unsigned long long cand =
+            (static_cast<unsigned long long>(so) << 32) | (~static_cast<uint32_t>(i0 + e));
+        bestk = cand > bestk ? cand : bestk;
+      }
     }
   });
 #pragma unroll

@@ -37,7 +37,8 @@ def test_greedy_rows_equal_argmax(gpu):
 
 @pytest.mark.parametrize("V,top_k,top_p,temp", [(151936, 50, 0.9, 1.0), (151936, 0, 0.8, 0.7),
                                                  (4000, 1000, 1.0, 1.2), (4000, 0, 1.0, 0.9),
-                                                 (1001, 7, 0.5, 1.0)])
+                                                 (1001, 7, 0.5, 1.0), (4000, 0, 0.0, 1.0),
+                                                 (151936, 20, -0.5, 1.0)])
 def test_sampled_tokens_stay_in_the_kept_set(gpu, V, top_k, top_p, temp):
     from qwen3_engine_from_scratch_amd.sampling import sample_tokens
 
