@@ -27,7 +27,13 @@
 // 4096 high bins keep the LDS atomics of a wave mostly on distinct
 // addresses (logits crowd into a few binades: 256 bins of sign + exponent
 // would serialise them), and the boundary bins are found by a block-wide
-// scan over four bins per thread.
+// scan over four bins per thread.  A pass over the row costs far more than
+// the work on it (one workgroup streams the whole row), so as soon as the
+// tokens that can still be kept fit in LDS (the bins at or above the top-k
+// boundary after A, or above the top-p boundary after C) the pass that finds
+// the boundary also appends them to a candidate list, and the later passes
+// and the draw run over that list; ranks among the ties at a partial cut come
+// from the tie indices themselves.
 // Masses are summed as 64-bit fixed point (2^40 per unit), so every
 // histogram and the cut are independent of summation order.
 #include "common.hpp"
@@ -88,6 +94,7 @@ constexpr int kLoBits = 4;
 constexpr int kLoBins = 1 << kLoBits;              // 16
 constexpr int kHiBins = 1 << (16 - kLoBits);       // 4096
 constexpr int kBinsPerThread = kHiBins / kThreads;  // 4
+constexpr int kCap = 4096;  // candidate list entries
 
 struct Shared {
   uint32_t cnt[kHiBins];
@@ -100,6 +107,10 @@ struct Shared {
   unsigned long long best[kWaves];
   int sel_bin;
   unsigned long long sel_run;
+  unsigned long long cand[kCap];  // candidate list: (key << 32) | token index
+  uint32_t ties[kThreads];        // indices of the ties at the cut
+  int ncand, nties;
+  uint32_t idx_cut;
 };
 
 // Block-wide sums; every thread gets the result.
@@ -330,9 +341,57 @@ __global__ __launch_bounds__(kThreads) void sample_kernel(const uint16_t* logits
   const bool use_p = pcut < 1.f;
   const float inv_t = 1.f / temp;
 
+  // Appends (key, index) of the lanes where q holds to the candidate list:
+  // one LDS atomic per wave.  Called by every lane of the wave.
+  auto compact = [&](bool q, uint32_t key, int64_t idx) {
+    const unsigned long long m = __ballot(q);
+    if (m == 0ull) return;
+    const int leader = __ffsll(static_cast<long long>(m)) - 1;
+    int base = 0;
+    if (lane == leader) base = atomicAdd(&sh.ncand, __popcll(m));
+    base = __shfl(base, leader, 64);
+    if (q) {
+      const int pos = base + __popcll(m & ((1ull << lane) - 1ull));
+      if (pos < kCap)
+        sh.cand[pos] = (static_cast<unsigned long long>(key) << 32) | static_cast<uint32_t>(idx);
+    }
+  };
+  // Once the candidate list holds every token that can still be kept
+  // (ncand >= 0), the later passes visit it instead of the row.
+  int ncand = -1;
+  auto visit = [&](auto&& f) {
+    if (ncand >= 0) {
+      for (int i = tid; i < ncand; i += kThreads) {
+        const unsigned long long c = sh.cand[i];
+        f(static_cast<uint32_t>(c >> 32), static_cast<int64_t>(static_cast<uint32_t>(c)));
+      }
+    } else {
+      for_each_round<kVec>(p, vocab, [&](int64_t i0, const uint32_t* b) {
+#pragma unroll
+        for (int e = 0; e < 8; ++e)
+          if (i0 + e < vocab) f(okey(b[e]), i0 + e);
+      });
+    }
+  };
+  // Tokens of the high bins >= hb, from the pass-A histogram (every thread
+  // gets the sum).
+  auto count_from = [&](int hb) {
+    const int top = kHiBins - 1 - kBinsPerThread * tid;
+    int c = 0;
+#pragma unroll
+    for (int j = 0; j < kBinsPerThread; ++j) c += top - j >= hb ? static_cast<int>(sh.cnt[top - j]) : 0;
+    return block_sum_int(c, sh);
+  };
+  auto finish_compaction = [&]() {
+    __syncthreads();
+    const int n = sh.ncand;
+    ncand = n <= kCap ? n : -1;
+  };
+
   // ---- A: high-bin counts and the maximum key ----------------------------
   for (int i = tid; i < kHiBins; i += kThreads) sh.cnt[i] = 0;
   if (tid < kLoBins) sh.lo_cnt[tid] = 0;
+  if (tid == 0) sh.ncand = 0;
   __syncthreads();
   uint32_t kmax = 0;
   for_each_round<kVec>(p, vocab, [&](int64_t i0, const uint32_t* b) {
@@ -362,14 +421,19 @@ __global__ __launch_bounds__(kThreads) void sample_kernel(const uint16_t* logits
   if (k < vocab) {
     int64_t above = 0;
     const int hb = find_count_bin_block(sh.cnt, k, above, sh);
+    // the tokens of bins >= hb hold the top-k list: keep them when they fit
+    const bool keep_list = above + static_cast<int64_t>(sh.cnt[hb]) <= kCap;
     for_each_round<kVec>(p, vocab, [&](int64_t i0, const uint32_t* b) {
 #pragma unroll
       for (int e = 0; e < 8; ++e) {
-        if (i0 + e >= vocab) break;
+        const bool valid = i0 + e < vocab;
         const uint32_t key = okey(b[e]);
-        if (static_cast<int>(key >> kLoBits) == hb) atomicAdd(&sh.lo_cnt[key & (kLoBins - 1)], 1u);
+        const int kb = static_cast<int>(key >> kLoBits);
+        if (valid && kb == hb) atomicAdd(&sh.lo_cnt[key & (kLoBins - 1)], 1u);
+        if (keep_list) compact(valid && kb >= hb, key, i0 + e);
       }
     });
+    if (keep_list) finish_compaction();
     __syncthreads();
     const int lb = find_count_bin(sh.lo_cnt, k, above);
     kk = (static_cast<uint32_t>(hb) << kLoBits) | static_cast<uint32_t>(lb);
@@ -395,16 +459,11 @@ __global__ __launch_bounds__(kThreads) void sample_kernel(const uint16_t* logits
     __syncthreads();
     const bool partial_k = k < vocab && tk < kties;
     const float wk = __expf(key_value(kk) * inv_t - xmax);
-    for_each_round<kVec>(p, vocab, [&](int64_t i0, const uint32_t* b) {
-#pragma unroll
-      for (int e = 0; e < 8; ++e) {
-        if (i0 + e >= vocab) break;
-        const uint32_t key = okey(b[e]);
-        if (key < kk || (partial_k && key == kk)) continue;
-        const float w = __expf(key_value(key) * inv_t - xmax);
-        atomicAdd(&sh.mass[key >> kLoBits],
-                  static_cast<unsigned long long>(static_cast<double>(w) * kFix + 0.5));
-      }
+    visit([&](uint32_t key, int64_t) {
+      if (key < kk || (partial_k && key == kk)) return;
+      const float w = __expf(key_value(key) * inv_t - xmax);
+      atomicAdd(&sh.mass[key >> kLoBits],
+                static_cast<unsigned long long>(static_cast<double>(w) * kFix + 0.5));
     });
     __syncthreads();
     const unsigned long long wk_fix =
@@ -417,48 +476,60 @@ __global__ __launch_bounds__(kThreads) void sample_kernel(const uint16_t* logits
     unsigned long long above_hi;
     const int hb = find_mass_bin_block(sh.mass, pcut, limit, above_hi, sh);
     if (hb >= 0) {  // else a row without mass (all NaN): no cut
-    for_each_round<kVec>(p, vocab, [&](int64_t i0, const uint32_t* b) {
-#pragma unroll
-      for (int e = 0; e < 8; ++e) {
-        if (i0 + e >= vocab) break;
-        const uint32_t key = okey(b[e]);
-        if (static_cast<int>(key >> kLoBits) != hb || key < kk) continue;
+      auto lo_hist = [&](uint32_t key, int64_t) {
+        if (static_cast<int>(key >> kLoBits) != hb || key < kk) return;
         atomicAdd(&sh.lo_cnt[key & (kLoBins - 1)], 1u);
-        if (partial_k && key == kk) continue;
+        if (partial_k && key == kk) return;
         const float w = __expf(key_value(key) * inv_t - xmax);
         atomicAdd(&sh.lo_mass[key & (kLoBins - 1)],
                   static_cast<unsigned long long>(static_cast<double>(w) * kFix + 0.5));
+      };
+      if (ncand >= 0) {
+        visit(lo_hist);
+      } else {
+        // the tokens that can be kept lie in bins >= hb: keep them when they fit
+        const bool keep_list = count_from(hb) <= kCap;
+        for_each_round<kVec>(p, vocab, [&](int64_t i0, const uint32_t* b) {
+#pragma unroll
+          for (int e = 0; e < 8; ++e) {
+            const bool valid = i0 + e < vocab;
+            const uint32_t key = okey(b[e]);
+            if (valid) lo_hist(key, i0 + e);
+            if (keep_list)
+              compact(valid && static_cast<int>(key >> kLoBits) >= hb && key >= kk, key, i0 + e);
+          }
+        });
+        if (keep_list) finish_compaction();
       }
-    });
-    __syncthreads();
-    if (partial_k && static_cast<int>(kk >> kLoBits) == hb && tid == 0) {
-      sh.lo_mass[kk & (kLoBins - 1)] += wk_fix * static_cast<unsigned long long>(tk);
-      sh.lo_cnt[kk & (kLoBins - 1)] = static_cast<uint32_t>(tk);
-    }
-    __syncthreads();
-    unsigned long long r2 = above_hi;
-    for (int bin = kLoBins - 1; bin >= 0; --bin) {
-      const unsigned long long m = sh.lo_mass[bin];
-      if (sh.lo_cnt[bin] == 0) continue;
-      if (static_cast<double>(r2 + m) > limit) {
-        // ties at this key: keep rank r while the mass before it, r2 +
-        // r * w, is within the limit (rank 0 of the list's first key is
-        // always kept since r2 is then 0)
-        const uint32_t key = (static_cast<uint32_t>(hb) << kLoBits) | static_cast<uint32_t>(bin);
-        const unsigned long long w = m / sh.lo_cnt[bin];
-        int64_t keep = 0;
-        while (keep < static_cast<int64_t>(sh.lo_cnt[bin]) &&
-               static_cast<double>(r2 + w * static_cast<unsigned long long>(keep)) <= limit)
-          ++keep;
-        if (keep == 0) keep = 1;  // cannot happen unless rounding: keep the first
-        // the top-p cut is inside the top-k list (its key >= kk)
-        kc = key;
-        cties = key == kk ? kties : sh.lo_cnt[bin];
-        tc = key == kk ? (keep < tk ? keep : tk) : keep;
-        break;
+      __syncthreads();
+      if (partial_k && static_cast<int>(kk >> kLoBits) == hb && tid == 0) {
+        sh.lo_mass[kk & (kLoBins - 1)] += wk_fix * static_cast<unsigned long long>(tk);
+        sh.lo_cnt[kk & (kLoBins - 1)] = static_cast<uint32_t>(tk);
       }
-      r2 += m;
-    }
+      __syncthreads();
+      unsigned long long r2 = above_hi;
+      for (int bin = kLoBins - 1; bin >= 0; --bin) {
+        const unsigned long long m = sh.lo_mass[bin];
+        if (sh.lo_cnt[bin] == 0) continue;
+        if (static_cast<double>(r2 + m) > limit) {
+          // ties at this key: keep rank r while the mass before it, r2 +
+          // r * w, is within the limit (rank 0 of the list's first key is
+          // always kept since r2 is then 0)
+          const uint32_t key = (static_cast<uint32_t>(hb) << kLoBits) | static_cast<uint32_t>(bin);
+          const unsigned long long w = m / sh.lo_cnt[bin];
+          int64_t keep = 0;
+          while (keep < static_cast<int64_t>(sh.lo_cnt[bin]) &&
+                 static_cast<double>(r2 + w * static_cast<unsigned long long>(keep)) <= limit)
+            ++keep;
+          if (keep == 0) keep = 1;  // cannot happen unless rounding: keep the first
+          // the top-p cut is inside the top-k list (its key >= kk)
+          kc = key;
+          cties = key == kk ? kties : sh.lo_cnt[bin];
+          tc = key == kk ? (keep < tk ? keep : tk) : keep;
+          break;
+        }
+        r2 += m;
+      }
     }
   }
 
@@ -466,49 +537,95 @@ __global__ __launch_bounds__(kThreads) void sample_kernel(const uint16_t* logits
   // kept: key > kc, or key == kc with tie rank < tc (no rank needed when all
   // ties are kept, or when the cut is at a key nothing ties with)
   const bool need_rank = tc < cties;
-  int64_t ties_before = 0;
   unsigned long long bestk = 0;  // (ordered score, complemented index)
-  for_each_round<kVec>(p, vocab, [&](int64_t i0, const uint32_t* b) {
-    int rank0 = 0;
+  auto offer = [&](uint32_t key, int64_t idx, uint32_t draw) {
+    const float sc = key_value(key) * inv_t + gumbel_of(draw);
+    const uint32_t sb = __float_as_uint(sc);
+    const uint32_t so = (sb & 0x80000000u) ? ~sb : (sb | 0x80000000u);
+    const unsigned long long c =
+        (static_cast<unsigned long long>(so) << 32) | (~static_cast<uint32_t>(idx));
+    bestk = c > bestk ? c : bestk;
+  };
+  if (ncand >= 0 && (!need_rank || cties <= kThreads)) {
+    // from the candidate list; with a partial tie, the tc-th smallest index
+    // of the ties at kc bounds the kept ones
+    uint32_t idx_cut = 0xFFFFFFFFu;
     if (need_rank) {
-      int c = 0;
-#pragma unroll
-      for (int e = 0; e < 8; ++e) c += (i0 + e < vocab && okey(b[e]) == kc) ? 1 : 0;
-      int total;
-      rank0 = block_scan_int(c, total, sh);
-      rank0 += static_cast<int>(ties_before);
-      ties_before += total;
-    }
-    int r = rank0;
-    bool kept[8];
-#pragma unroll
-    for (int e = 0; e < 8; ++e) {
-      const uint32_t key = okey(b[e]);
-      bool kp = key > kc;
-      if (key == kc && i0 + e < vocab) {
-        kp = !need_rank || r < tc;
-        ++r;
+      if (tid == 0) {
+        sh.nties = 0;
+        sh.idx_cut = 0xFFFFFFFFu;
       }
-      kept[e] = kp && key != 0 && i0 + e < vocab;
-    }
-    // one Philox block per four tokens (i0 is a multiple of 8)
-#pragma unroll
-    for (int h = 0; h < 2; ++h) {
-      if (!(kept[4 * h] || kept[4 * h + 1] || kept[4 * h + 2] || kept[4 * h + 3])) continue;
-      const q3::u32x4 d = draws4(seed, row, (i0 >> 2) + h);
-#pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        const int e = 4 * h + j;
-        if (!kept[e]) continue;
-        const float sc = key_value(okey(b[e])) * inv_t + gumbel_of(d[j]);
-        const uint32_t sb = __float_as_uint(sc);
-        const uint32_t so = (sb & 0x80000000u) ? ~sb : (sb | 0x80000000u);
-        const unsigned long long cand =
-            (static_cast<unsigned long long>(so) << 32) | (~static_cast<uint32_t>(i0 + e));
-        bestk = cand > bestk ? cand : bestk;
+      __syncthreads();
+      for (int i0 = 0; i0 < ncand; i0 += kThreads) {
+        const int i = i0 + tid;
+        const unsigned long long c = i < ncand ? sh.cand[i] : 0ull;
+        const bool q = i < ncand && static_cast<uint32_t>(c >> 32) == kc;
+        const unsigned long long m = __ballot(q);
+        if (m == 0ull) continue;
+        const int leader = __ffsll(static_cast<long long>(m)) - 1;
+        int base = 0;
+        if (lane == leader) base = atomicAdd(&sh.nties, __popcll(m));
+        base = __shfl(base, leader, 64);
+        if (q) {
+          const int pos = base + __popcll(m & ((1ull << lane) - 1ull));
+          if (pos < kThreads) sh.ties[pos] = static_cast<uint32_t>(c);
+        }
       }
+      __syncthreads();
+      const int nt = sh.nties < kThreads ? sh.nties : kThreads;
+      if (tid < nt) {
+        const uint32_t mine = sh.ties[tid];
+        int rank = 0;
+        for (int j = 0; j < nt; ++j) rank += sh.ties[j] < mine ? 1 : 0;
+        if (rank == tc - 1) sh.idx_cut = mine;
+      }
+      __syncthreads();
+      idx_cut = sh.idx_cut;
     }
-  });
+    for (int i = tid; i < ncand; i += kThreads) {
+      const unsigned long long c = sh.cand[i];
+      const uint32_t key = static_cast<uint32_t>(c >> 32);
+      const uint32_t idx = static_cast<uint32_t>(c);
+      const bool kept = key > kc || (key == kc && idx <= idx_cut);
+      if (!kept || key == 0) continue;
+      offer(key, idx, draws4(seed, row, idx >> 2)[idx & 3]);
+    }
+  } else {
+    int64_t ties_before = 0;
+    for_each_round<kVec>(p, vocab, [&](int64_t i0, const uint32_t* b) {
+      int rank0 = 0;
+      if (need_rank) {
+        int c = 0;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) c += (i0 + e < vocab && okey(b[e]) == kc) ? 1 : 0;
+        int total;
+        rank0 = block_scan_int(c, total, sh);
+        rank0 += static_cast<int>(ties_before);
+        ties_before += total;
+      }
+      int r = rank0;
+      bool kept[8];
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        const uint32_t key = okey(b[e]);
+        bool kp = key > kc;
+        if (key == kc && i0 + e < vocab) {
+          kp = !need_rank || r < tc;
+          ++r;
+        }
+        kept[e] = kp && key != 0 && i0 + e < vocab;
+      }
+      // one Philox block per four tokens (i0 is a multiple of 8)
+#pragma unroll
+      for (int h = 0; h < 2; ++h) {
+        if (!(kept[4 * h] || kept[4 * h + 1] || kept[4 * h + 2] || kept[4 * h + 3])) continue;
+        const q3::u32x4 d = draws4(seed, row, (i0 >> 2) + h);
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+          if (kept[4 * h + j]) offer(okey(b[4 * h + j]), i0 + 4 * h + j, d[j]);
+      }
+    });
+  }
 #pragma unroll
   for (int m = 1; m < 64; m <<= 1) {
     const unsigned long long o = __shfl_xor(bestk, m, 64);

@@ -38,7 +38,8 @@ def test_greedy_rows_equal_argmax(gpu):
 @pytest.mark.parametrize("V,top_k,top_p,temp", [(151936, 50, 0.9, 1.0), (151936, 0, 0.8, 0.7),
                                                  (4000, 1000, 1.0, 1.2), (4000, 0, 1.0, 0.9),
                                                  (1001, 7, 0.5, 1.0), (4000, 0, 0.0, 1.0),
-                                                 (151936, 20, -0.5, 1.0)])
+                                                 (151936, 20, -0.5, 1.0), (151936, 5000, 1.0, 1.0),
+                                                 (151936, 3000, 0.95, 1.0)])
 def test_sampled_tokens_stay_in_the_kept_set(gpu, V, top_k, top_p, temp):
     from qwen3_engine_from_scratch_amd.sampling import sample_tokens
 
@@ -52,6 +53,48 @@ def test_sampled_tokens_stay_in_the_kept_set(gpu, V, top_k, top_p, temp):
         out = out.cpu().view(-1).tolist()
         for r in range(B):
             assert out[r] in kept[r], (r, out[r])
+
+
+@pytest.mark.parametrize("n_ties,top_k", [(2000, 1500), (1000, 900), (300, 0)])
+def test_partial_cut_inside_many_ties(gpu, n_ties, top_k):
+    """Many tokens share the top value: a top-k cut inside them keeps the
+    lowest indices (more ties than one per thread takes the row pass); with
+    top_k 0, a top-p cut inside them does the same."""
+    from qwen3_engine_from_scratch_amd.sampling import sample_tokens
+
+    announce(f"sampling: cut inside {n_ties} ties, top_k={top_k}")
+    V, B = 8192, 32
+    g = torch.Generator().manual_seed(n_ties)
+    x = torch.full((V,), -8.0)
+    x[torch.randperm(V, generator=g)[:n_ties]] = 3.0
+    x = x.to(torch.bfloat16)
+    top_p = 1.0 if top_k else 0.5
+    kept = osm.kept_set(x.float(), 1.0, top_k, top_p)
+    assert len(kept) == (top_k if top_k else n_ties // 2 + 1)
+    out = sample_tokens(x.expand(B, V).contiguous().to(gpu), temperature=1.0, top_k=top_k,
+                        top_p=top_p, seed=9)
+    got = out.cpu().view(-1).tolist()
+    assert all(t in kept for t in got), sorted(set(got) - kept)[:5]
+
+
+def test_peaked_top_p_row(gpu):
+    """A peaked row (few tokens carry the mass): the top-p pass keeps the
+    candidates in LDS; draws stay in the kept set and follow it."""
+    from qwen3_engine_from_scratch_amd.sampling import sample_tokens
+
+    announce("sampling: peaked top-p")
+    V, N = 151936, 4096
+    g = torch.Generator().manual_seed(4)
+    row = (torch.randn(V, generator=g) * 1.0)
+    row[:12] += torch.linspace(14.0, 10.0, 12)
+    row = row.to(torch.bfloat16)
+    p = osm.sampling_distribution(row.float(), 1.0, 0, 0.9)
+    out = sample_tokens(row.to(gpu).expand(N, V).contiguous(), temperature=1.0, top_p=0.9, seed=2)
+    got = out.cpu().view(-1).numpy()
+    assert (p[got] > 0).all()
+    counts = np.bincount(got, minlength=V)[:12] / N
+    tol = 5 * np.sqrt(p[:12] * (1 - p[:12]) / N) + 2.0 / N
+    assert (np.abs(counts - p[:12]) <= tol).all()
 
 
 @pytest.mark.parametrize("top_k,top_p,temp", [(0, 1.0, 1.0), (10, 1.0, 0.8), (0, 0.75, 1.0),
