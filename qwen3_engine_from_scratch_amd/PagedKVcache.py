@@ -16,6 +16,7 @@ one (block, layer, head) chunk is block_size * head_dim contiguous bf16
 """
 from __future__ import annotations
 
+import numpy as np
 import torch
 
 from . import _lib
@@ -185,7 +186,6 @@ class PagedKVCache:
         """Reserves the pages of positions seq_len .. seq_len + n - 1 (as
         update does, :186-190) and returns their pool slots, block *
         block_size + offset, as an int64 numpy array."""
-        import numpy as np
 
         bs = self._pool.block_size
         end = self.seq_len + n
@@ -245,15 +245,19 @@ class PageIn:
         ids = pool.take_blocks(total)
         h = self._host[self._flip]
         self._flip ^= 1
+        # rows | page columns | block ids, filled through a numpy view of the
+        # pinned buffer (element-wise tensor writes cost microseconds each)
+        hn = h.numpy()
+        counts = [k for _, k in want]
+        hn[:total] = np.repeat([c.row_id for c, _ in want], counts)
+        hn[total:2 * total] = np.concatenate(
+            [np.arange(c.num_pages, c.num_pages + k) for c, k in want])
+        hn[2 * total:3 * total] = ids
         i = 0
         for c, k in want:
-            for j in range(k):
-                h[i] = c.row_id
-                h[total + i] = c.num_pages + j
-                h[2 * total + i] = ids[i]
-                i += 1
-            c.block_table.extend(ids[i - k:i])
+            c.block_table.extend(ids[i:i + k])
             c.num_pages += k
+            i += k
         d = self._dev[:3 * total]
         d.copy_(h[:3 * total], non_blocking=True)
         bt = pool.block_table_2d
@@ -311,8 +315,6 @@ def prefill_slot_mapping(caches, S: int, device) -> torch.Tensor:
     batch: the reference's per-request update writes all S positions from
     each request's seq_len (pads included, qwen3/attention.py:160-161), so the
     mapping covers them too.  Reserves the pages the same way."""
-    import numpy as np
-
     bs = caches[0]._pool.block_size
     slots = np.empty((len(caches), S), dtype=np.int64)
     pos = np.arange(S, dtype=np.int64)
