@@ -230,3 +230,30 @@ def test_decode_config1_golden_fixture(gpu):
     out, _ = _run(case, gpu)
     assert_close_attn(out, torch.from_numpy(f["dense_fp64"]), "golden fp64")
     assert_close_attn(out, torch.from_numpy(f["oracle_fp32"]), "golden oracle")
+
+
+@pytest.mark.parametrize("B,lo,hi", [(64, 500, 900), (6, 20, 300)])
+def test_decode_garbage_workspace_same_bits(gpu, B, lo, hi):
+    """The split-KV workspace carries no state between calls: a workspace
+    full of 0xFF bytes gives the same bits as a zeroed one, and so does a
+    second call on the same workspace."""
+    from qwen3_engine_from_scratch_amd.kernels.paged_attention import (
+        paged_attention_decode_hip, paged_decode_workspace_bytes)
+
+    g = torch.Generator().manual_seed(B)
+    lens = [int(x) for x in torch.randint(lo, hi, (B,), generator=g)]
+    announce(f"decode garbage workspace B={B} lens in [{lo},{hi})")
+    t = make_device_decode(lens, 16, 8, gpu, seed=B, slack=0.1)
+    need = paged_decode_workspace_bytes(B, 16, 128, t["bt"].shape[1], 16)
+    outs = []
+    ws = None
+    for fill in (0, 255, None):
+        if fill is not None:
+            ws = torch.full((need,), fill, dtype=torch.uint8, device=gpu)
+        out = paged_attention_decode_hip(t["q"], t["k"], t["v"], t["bt"], t["seq_lens"],
+                                         t["row_ids"], 16, workspace=ws)
+        torch.cuda.synchronize()
+        outs.append(out.cpu())
+    assert torch.equal(outs[0], outs[1]) and torch.equal(outs[0], outs[2])
+    ref = gpu_dense_decode_fp32(t["q"], t["k"], t["v"], t["bt"], t["seq_lens"], t["row_ids"], 16)
+    assert_close_attn(outs[0], ref, "garbage workspace")
