@@ -28,6 +28,10 @@
  *   qwen3_embed_ss_bf16     <- the embedding lookup (qwen3/model.py:212) writing
  *                              the residual stream and its partial sums of squares
  *                              for the fused first norm
+ *   qwen3_lm_head_argmax_bf16 <- the final norm, lm_head and greedy choice of a
+ *                              decode step (qwen3/model.py:217,241 and
+ *                              qwen3/sampling.py:256-258) in one pass over the
+ *                              tied embedding, without the logits
  *   qwen3_page_in_bf16      <- the device writes of KVCachePool.alloc (zeroing a
  *                              reused block, qwen3/PagedKVcache.py:58-73) and of
  *                              PagedKVCache._allocate_block (the resident table
@@ -174,6 +178,22 @@ int qwen3_sample_bf16(const void* logits, int64_t row_stride, int64_t rows, int6
  * lengths; this keeps the resident table in step without a host write. */
 int qwen3_advance_seq_lens(int32_t* seq_lens, int64_t max_rows, const int32_t* row_ids,
                            int n, int skip_row, int delta, void* stream);
+
+/* Workspace (device, 16-byte aligned) that qwen3_lm_head_argmax_bf16 needs:
+ * per-workgroup row maxima.  Its contents need no initialisation. */
+size_t qwen3_lm_head_argmax_workspace_bytes(void);
+
+/* Greedy decode head for M <= 64 rows: a = RMSNorm(h) with the rms taken
+ * from ss_in (as qwen3_decode_linear_bf16's norm prologue) and norm_weight,
+ * logits = bf16(a @ weight^T) over vocab rows of weight (M x vocab, never
+ * stored), out[r] (int64) = the first index of the largest logit of row r
+ * (NaN ranks highest, as qwen3_argmax_bf16).  K a multiple of 512, at most
+ * 1024.  Two launches (one workgroup per CU, then the per-row reduction). */
+int qwen3_lm_head_argmax_bf16(const void* h, int64_t h_row_stride, const float* ss_in,
+                              int ss_in_tiles, const void* norm_weight, float eps,
+                              const void* weight, int64_t weight_row_stride, int M, int vocab,
+                              int K, void* workspace, size_t workspace_bytes, int64_t* out,
+                              void* stream);
 
 #ifdef __cplusplus
 }

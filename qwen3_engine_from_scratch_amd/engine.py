@@ -171,8 +171,7 @@ class Engine:
         else:
             ids = torch.tensor([r.output_ids[-1] for r in reqs], dtype=torch.int64).to(dev)
             rows = torch.tensor([c.row_id for c in caches], dtype=torch.int32).to(dev)
-            logits = self.model.decode_logits(ids, rows, self.pool)
-            toks = argmax(logits)
+            toks = self.model.decode_greedy(ids, rows, self.pool)
         host = self._tok_host[self._flip][:k]
         self._flip ^= 1
         host.copy_(toks, non_blocking=True)

@@ -10,9 +10,12 @@ through torch.cuda.graph on torch's current stream, which is the stream
 every kernel of this package launches on.
 
 Two optional stages, used by the batching engine, ride in the same graph:
-  greedy=True    the greedy choice (HIP argmax) is written straight into the
-                 captured input ids, so the next step's inputs are already in
-                 place and only the tokens come back to the host;
+  greedy=True    the step ends in the greedy choice instead of logits (the
+                 model's decode_greedy: final norm, lm_head and argmax in one
+                 pass over the tied embedding on the fused path) written
+                 straight into the captured input ids, so the next step's
+                 inputs are already in place and only the tokens come back
+                 to the host (replay_greedy; such a runner has no logits);
   advance=True   the resident seq_lens of the batch's rows are advanced by
                  one on the device (the dummy row excepted), replacing the
                  host's per-request writes of advance_seq_len.
@@ -24,7 +27,7 @@ from __future__ import annotations
 
 import torch
 
-from .kernels.model_ops import advance_seq_lens, argmax
+from .kernels.model_ops import advance_seq_lens
 
 __all__ = ["GraphRunner", "pow2_buckets"]
 
@@ -73,10 +76,12 @@ class GraphRunner:
 
     def _step(self, t, caches):
         pos = None if self.positions_from_lengths else t["pos"]
-        logits = self.model.forward_decode(t["input"], pos, t["rows"], caches)
         if self.greedy:
-            argmax(logits.view(logits.shape[0], -1), out=t["input"].view(-1))
-        return logits
+            ids = t["input"].view(-1)
+            self.model.decode_greedy(ids, t["rows"], self.pool,
+                                     None if pos is None else pos.view(-1), out=ids)
+            return None
+        return self.model.forward_decode(t["input"], pos, t["rows"], caches)
 
     @torch.no_grad()
     def _capture_all(self, caches):
@@ -106,6 +111,7 @@ class GraphRunner:
         """Reference entry (qwen3/graph_runner.py:165-200): input_ids,
         positions (k, 1) int64 and rows (k,) int32 of this step; returns the
         bucket's logits (b, 1, V), the first k rows valid."""
+        assert not self.greedy, "a greedy runner returns tokens: use replay_greedy"
         k = input_ids.shape[0]
         b = self.bucket_for(k)
         g, t = self.graphs[b]

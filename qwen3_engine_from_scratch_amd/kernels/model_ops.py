@@ -15,9 +15,11 @@ import torch
 from .. import _lib
 
 __all__ = ["add_rms_norm", "embed_rms_norm", "silu_mul", "argmax", "advance_seq_lens",
+           "lm_head_argmax", "LM_HEAD_ARGMAX_MAX_K",
            "decode_linear", "decode_qkv_rope", "embed_ss", "DECODE_LINEAR_MAX_ROWS"]
 
 DECODE_LINEAR_MAX_ROWS = 64
+LM_HEAD_ARGMAX_MAX_K = 1024
 _EPI = {"store": 0, "residual": 1, "silu": 2}
 
 
@@ -114,6 +116,45 @@ def argmax(logits: torch.Tensor, out: torch.Tensor | None = None) -> torch.Tenso
     rc = _lib.load().qwen3_argmax_bf16(logits.data_ptr(), logits.stride(0), rows, vocab,
                                        out.data_ptr(), _lib.stream_of(dev))
     _lib.check(rc, "qwen3_argmax_bf16")
+    return out
+
+
+def lm_head_argmax_ok(hidden: int) -> bool:
+    """Whether lm_head_argmax handles this hidden size."""
+    return hidden % 512 == 0 and hidden <= LM_HEAD_ARGMAX_MAX_K
+
+
+def lm_head_argmax(h: torch.Tensor, ss_in: torch.Tensor, norm_weight: torch.Tensor, eps: float,
+                   weight: torch.Tensor, *, out: torch.Tensor | None = None,
+                   workspace: torch.Tensor | None = None) -> torch.Tensor:
+    """Greedy tokens of a decode step, (M,) int64, for M <= 64 rows of the
+    residual stream h (M, K) bf16: argmax over the vocabulary of
+    bf16(RMSNorm(h) @ weight^T), the rms taken from ss_in (M, K/16) fp32
+    per-16-column sums of h^2 (written by the last residual epilogue), in
+    one pass over weight (V, K) without storing the logits.  Ties take the
+    first index and NaN ranks highest (torch.argmax's rule)."""
+    h = _rows2d(h)
+    M, K = h.shape
+    V = weight.shape[0]
+    assert h.dtype == torch.bfloat16 and weight.dtype == torch.bfloat16
+    assert norm_weight.dtype == torch.bfloat16 and norm_weight.is_contiguous()
+    assert ss_in.dtype == torch.float32 and ss_in.is_contiguous() and ss_in.shape[0] == M
+    assert weight.shape[1] == K and weight.stride(1) == 1
+    assert M <= DECODE_LINEAR_MAX_ROWS and lm_head_argmax_ok(K)
+    dev = _lib.require_hip(h, ss_in, norm_weight, weight, out, workspace)
+    if out is None:
+        out = torch.empty(M, dtype=torch.int64, device=h.device)
+    assert out.dtype == torch.int64 and out.is_contiguous() and out.numel() == M
+    lib = _lib.load()
+    need = int(lib.qwen3_lm_head_argmax_workspace_bytes())
+    if workspace is None or workspace.numel() < need:
+        workspace = torch.empty(need, dtype=torch.uint8, device=h.device)
+    rc = lib.qwen3_lm_head_argmax_bf16(h.data_ptr(), h.stride(0), ss_in.data_ptr(),
+                                       ss_in.shape[1], norm_weight.data_ptr(), float(eps),
+                                       weight.data_ptr(), weight.stride(0), M, V, K,
+                                       workspace.data_ptr(), workspace.numel(), out.data_ptr(),
+                                       _lib.stream_of(dev))
+    _lib.check(rc, "qwen3_lm_head_argmax_bf16")
     return out
 
 

@@ -33,8 +33,10 @@ import torch.nn.functional as F
 
 from .config import Qwen3Config
 from .kernels.flash_attention_varlen import flash_attention_prefill
-from .kernels.model_ops import (DECODE_LINEAR_MAX_ROWS, add_rms_norm, decode_linear,
-                                decode_qkv_rope, embed_rms_norm, embed_ss, silu_mul)
+from .kernels.model_ops import (DECODE_LINEAR_MAX_ROWS, add_rms_norm, argmax, decode_linear,
+                                decode_qkv_rope, embed_rms_norm, embed_ss, lm_head_argmax,
+                                lm_head_argmax_ok, silu_mul)
+from . import _lib
 from .kernels.paged_attention import paged_attention_decode_hip, paged_decode_workspace_bytes
 from .kernels.pre_attention import qk_norm_rope_decode, qk_norm_rope_prefill, rope_tables
 
@@ -133,6 +135,7 @@ class Qwen3ForCausalLM(nn.Module):
         if config.tie_word_embeddings:
             self.lm_head.weight = self.model.embed_tokens.weight
         self._workspace = None
+        self._head_ws = None
 
     # ---- shared layer loop -------------------------------------------------
 
@@ -170,6 +173,9 @@ class Qwen3ForCausalLM(nn.Module):
         if self._workspace is None or self._workspace.numel() < need:
             self._workspace = torch.empty(max(need, 1), dtype=torch.uint8,
                                           device=pool.k_buffer.device)
+        if self._head_ws is None:
+            self._head_ws = torch.empty(int(_lib.load().qwen3_lm_head_argmax_workspace_bytes()),
+                                        dtype=torch.uint8, device=pool.k_buffer.device)
 
     def fused_decode_ok(self, batch: int) -> bool:
         """Whether a decode step of `batch` rows runs on the fused decode
@@ -180,12 +186,21 @@ class Qwen3ForCausalLM(nn.Module):
                 and c.head_dim == 128 and c.hidden_size <= 4096)
 
     def _decode_fused(self, ids, row_ids, pool, positions) -> torch.Tensor:
-        """Decode step on the fused kernels: the residual stream ping-pongs
-        between two buffers, each with its per-16-column sums of squares, so
-        every RMSNorm is the prologue of the linear after it and every
-        residual add the epilogue of the linear before it; the qkv
-        projection also applies QK-norm and RoPE and writes K/V into the
-        pool, leaving one attention launch (plus its merge) per layer."""
+        """Decode step on the fused kernels; returns the logits."""
+        h, _ = self._decode_layers(ids, row_ids, pool, positions)
+        # lm_head streams 311 MB of weights for few rows: the library GEMM
+        # after a separate final norm
+        final = add_rms_norm(None, h, self.model.norm.weight, self.config.rms_norm_eps)
+        return F.linear(final, self.lm_head.weight)
+
+    def _decode_layers(self, ids, row_ids, pool, positions):
+        """The decoder layers of a decode step on the fused kernels: the
+        residual stream ping-pongs between two buffers, each with its
+        per-16-column sums of squares, so every RMSNorm is the prologue of
+        the linear after it and every residual add the epilogue of the
+        linear before it; the qkv projection also applies QK-norm and RoPE
+        and writes K/V into the pool, leaving one attention launch (plus its
+        merge) per layer.  Returns the last residual stream and its sums."""
         cfg = self.config
         eps = cfg.rms_norm_eps
         layers = self.model.layers
@@ -210,10 +225,32 @@ class Qwen3ForCausalLM(nn.Module):
                                 norm_weight=layer.post_attention_layernorm.weight, eps=eps)
             decode_linear(act, layer.mlp.down_proj.weight, epilogue="residual",
                           residual=h_b, residual_out=h_a, ss_out=ss_a)
-        # lm_head streams 311 MB of weights for few rows: the library GEMM
-        # after a separate final norm
-        final = add_rms_norm(None, h_a, self.model.norm.weight, eps)
-        return F.linear(final, self.lm_head.weight)
+        return h_a, ss_a
+
+    @torch.no_grad()
+    def decode_greedy(self, ids: torch.Tensor, row_ids: torch.Tensor, pool,
+                      positions: torch.Tensor | None = None,
+                      out: torch.Tensor | None = None) -> torch.Tensor:
+        """Greedy tokens (B,) int64 of one decode step, argmax of
+        decode_logits(...).  On the fused path the final norm, lm_head and
+        argmax run as one pass over the tied embedding that never stores the
+        logits (qwen3_lm_head_argmax_bf16); out may alias ids (the ids are
+        read before the tokens are written)."""
+        B = ids.numel()
+        cfg = self.config
+        if out is None:
+            out = torch.empty(B, dtype=torch.int64, device=ids.device)
+        if self.fused_decode_ok(B) and lm_head_argmax_ok(cfg.hidden_size):
+            self.reserve_decode_workspace(B, pool)
+            rows = row_ids if row_ids is not None else torch.arange(
+                B, dtype=torch.int32, device=ids.device)
+            h, ss = self._decode_layers(ids.reshape(-1).contiguous(), rows.contiguous(), pool,
+                                        positions)
+            lm_head_argmax(h, ss, self.model.norm.weight, cfg.rms_norm_eps, self.lm_head.weight,
+                           out=out.view(-1), workspace=self._head_ws)
+            return out
+        logits = self.decode_logits(ids, row_ids, pool, positions)
+        return argmax(logits, out=out.view(-1))
 
     @torch.no_grad()
     def decode_logits(self, ids: torch.Tensor, row_ids: torch.Tensor, pool,

@@ -170,6 +170,15 @@ def test_model_ops_reject_bad_arguments():
 
     assert qkv(M=65) == -1 and qkv(D=64) == -3 and qkv(K=1000) == -3 and qkv(K=4160) == -3
     assert qkv(ss=None) == -1 and qkv(bt_stride=4) == -1
+    ws = lib.qwen3_lm_head_argmax_workspace_bytes()
+    assert ws > 0
+
+    def head(M=16, K=1024, wsb=ws, out=FAKE):
+        return lib.qwen3_lm_head_argmax_bf16(FAKE, K, FAKE, K // 16, FAKE, 1e-6, FAKE, K, M,
+                                             151936, K, FAKE, wsb, out, None)
+
+    assert head(M=65) == -1 and head(K=1000) == -3 and head(K=2048) == -3
+    assert head(wsb=ws - 1) == -4 and head(out=None) == -1 and head(M=0) == 0
     # nothing to do: no launch, success
     assert lib.qwen3_add_rms_norm_bf16(None, 0, FAKE, 1024, None, 0, FAKE, 1e-6, FAKE, 1024,
                                        None, 0, 0, 1024, None) == 0

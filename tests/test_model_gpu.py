@@ -263,6 +263,46 @@ def test_decode_qkv_rope_vs_oracle(gpu, M, K):
     assert int((kb[:, 1].abs().sum(-1) > 0).sum()) == written * Hkv, "only the new slots written"
 
 
+@pytest.mark.parametrize("M,V", [(1, 4096), (37, 1005), (64, 151936)])
+def test_lm_head_argmax_vs_reference(gpu, M, V):
+    """Final norm + lm_head + argmax in one pass: the chosen token's logit
+    (fp32 reference rounded to bf16) is the row maximum up to one bf16 step,
+    and the index equals the reference argmax except in near-ties."""
+    from qwen3_engine_from_scratch_amd.kernels.model_ops import lm_head_argmax
+
+    announce(f"lm_head argmax M={M} V={V}")
+    K = 1024
+    g = torch.Generator().manual_seed(M + V)
+    h = (torch.randn(M, K, generator=g) * 2).to(torch.bfloat16)
+    wn = (1 + 0.1 * torch.randn(K, generator=g)).to(torch.bfloat16)
+    W = (torch.randn(V, K, generator=g) * 0.05).to(torch.bfloat16)
+    ss = (h.float() ** 2).view(M, K // 16, 16).sum(-1).contiguous()
+    out = lm_head_argmax(h.to(gpu), ss.to(gpu), wn.to(gpu), 1e-6, W.to(gpu)).cpu()
+    ref = (oi.rms_norm(h, wn, 1e-6).float() @ W.float().T).to(torch.bfloat16).float()
+    mx = ref.max(-1).values
+    got = ref.gather(1, out.view(-1, 1)).view(-1)
+    assert ((mx - got) <= mx.abs() * 2.0 ** -7 + 1e-6).all(), (mx - got).max()
+    assert (out == ref.argmax(-1)).float().mean() >= 0.9
+
+
+def test_lm_head_argmax_ties_and_nan(gpu):
+    """Equal largest logits take the first index; a NaN logit wins."""
+    from qwen3_engine_from_scratch_amd.kernels.model_ops import lm_head_argmax
+
+    announce("lm_head argmax ties and NaN")
+    M, K, V = 5, 512, 777
+    g = torch.Generator().manual_seed(3)
+    h = torch.ones(M, K, dtype=torch.bfloat16)
+    wn = torch.ones(K, dtype=torch.bfloat16)
+    W = (torch.randn(V, K, generator=g) * 0.01).to(torch.bfloat16)
+    W[20] = W[700] = 0.1
+    ss = (h.float() ** 2).view(M, K // 16, 16).sum(-1).contiguous()
+    args = (h.to(gpu), ss.to(gpu), wn.to(gpu), 1e-6)
+    assert lm_head_argmax(*args, W.to(gpu)).tolist() == [20] * M
+    W[300, 7] = float("nan")
+    assert lm_head_argmax(*args, W.to(gpu)).tolist() == [300] * M
+
+
 def test_page_in_maps_and_zeroes_blocks(gpu):
     from qwen3_engine_from_scratch_amd.PagedKVcache import KVCachePool, PageIn, PagedKVCache
 
