@@ -245,6 +245,155 @@ __global__ __launch_bounds__(kWaves * 64) void decode_linear_kernel(LinArgs a) {
   }
 }
 
+// The SwiGLU linear with its RMSNorm prologue for 17..64 rows: one
+// 512-thread workgroup per 16 output columns holding every row.  The rows
+// are normalised once into LDS (the row-block split above fetches the
+// normalised activations once per (row block, column tile) pair: 3x the
+// weight bytes of traffic per CU at 64 rows), the eight waves split K and
+// stream the gate and up weight tiles, and their partial tiles meet in the
+// same LDS space once the rows are no longer read.
+constexpr int kWaves64 = 8;
+constexpr int kMaxK64 = 1024;  // 64 x (K + 8) bf16 rows in LDS
+
+__global__ __launch_bounds__(kWaves64 * 64) void gate_up64_kernel(LinArgs a) {
+  extern __shared__ uint16_t a_s[];  // rows, then the cross-wave partial tiles
+  __shared__ float rms_s[64];
+  const int tile = blockIdx.x;
+  const int tid = threadIdx.x;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int lane = tid & 63;
+  const int r16 = lane & 15;
+  const int kg = 8 * (lane >> 4);
+  const int pitch = a.K + 8;
+  const int kw = a.K / kWaves64;
+  const int k0 = wave * kw;
+  const int steps = kw / kKStep;  // at most kMaxK64 / (8 x 32) = 4
+  const int n0 = tile * kTile;
+
+  // This wave's weight loads first: they do not depend on the rows.
+  const int lrow = lane >> 2, lkg = 8 * (lane & 3);
+  const int perm_addr = 4 * (4 * r16 + (lane >> 4));
+  const uint16_t* wg = a.w + static_cast<int64_t>(n0 + lrow) * a.w_s + lkg + k0;
+  const uint16_t* wu = a.w + static_cast<int64_t>(a.up_row + n0 + lrow) * a.w_s + lkg + k0;
+  constexpr int kMaxSteps = kMaxK64 / (kWaves64 * kKStep);
+  q3::u32x4 bg[kMaxSteps], bu[kMaxSteps];
+#pragma unroll
+  for (int u = 0; u < kMaxSteps; ++u) {
+    if (u >= steps) break;
+    bg[u] = q3::ld16(wg + u * kKStep);
+    bu[u] = q3::ld16(wu + u * kKStep);
+  }
+  // The rows of h, all loads in flight before the rms is known: chunk c =
+  // tid + i * threads of the 64 x K/8 16-byte chunks (at most 16 per thread
+  // for K <= 1024).  When the thread count is a multiple of the chunks per
+  // row, a thread's chunks share one column and so one norm-weight chunk.
+  constexpr int kChunksPerThread = 16;
+  const int cpr = a.K >> 3;
+  const int nch = 64 * cpr;
+  const bool one_col = (kWaves64 * 64) % cpr == 0;
+  q3::u32x4 hv[kChunksPerThread];
+  q3::u32x4 nv0 = {0u, 0u, 0u, 0u};
+  if (one_col) nv0 = q3::ld16(a.norm_w + 8 * (tid % cpr));
+#pragma unroll
+  for (int i = 0; i < kChunksPerThread; ++i) {
+    const int c = tid + i * (kWaves64 * 64);
+    if (c >= nch) break;
+    const int r = c / cpr, cc = c - r * cpr;
+    hv[i] = q3::ld16(a.x + static_cast<int64_t>(min(r, a.M - 1)) * a.x_s + 8 * cc);
+  }
+  // rms of every row from the producer's partial sums (as the kernel above)
+  if (tid < 256) {
+    const int row = min(tid >> 2, a.M - 1);
+    const int part = tid & 3;
+    const float* sp = a.ss_in + static_cast<int64_t>(row) * a.ss_in_tiles;
+    float s = 0.f;
+    if (a.ss_in_tiles == 64) {
+      float4 f[4];
+#pragma unroll
+      for (int j = 0; j < 4; ++j) f[j] = reinterpret_cast<const float4*>(sp + 16 * part)[j];
+#pragma unroll
+      for (int j = 0; j < 4; ++j) s += ((f[j].x + f[j].y) + f[j].z) + f[j].w;
+    } else {
+      for (int t = part; t < a.ss_in_tiles; t += 4) s += sp[t];
+    }
+    s += __shfl_xor(s, 1, 64);
+    s += __shfl_xor(s, 2, 64);
+    if (part == 0) rms_s[tid >> 2] = 1.f / sqrtf(s / static_cast<float>(a.K) + a.eps);
+  }
+  __syncthreads();
+  // a = bf16((h * rms) * w) for 64 rows (rows past M repeat M - 1)
+#pragma unroll
+  for (int i = 0; i < kChunksPerThread; ++i) {
+    const int c = tid + i * (kWaves64 * 64);
+    if (c >= nch) break;
+    const int r = c / cpr, cc = c - r * cpr;
+    const q3::u32x4 nv = one_col ? nv0 : q3::ld16(a.norm_w + 8 * cc);
+    const float rr = rms_s[r];
+    q3::u32x4 o;
+#pragma unroll
+    for (int e = 0; e < 4; ++e)
+      o[e] = q3::pack_bf16x2((q3::bf16_lo(hv[i][e]) * rr) * q3::bf16_lo(nv[e]),
+                             (q3::bf16_hi(hv[i][e]) * rr) * q3::bf16_hi(nv[e]));
+    *reinterpret_cast<q3::u32x4*>(a_s + r * pitch + 8 * cc) = o;
+  }
+  __syncthreads();
+
+  q3::f32x4 acc[4][2];
+#pragma unroll
+  for (int rb = 0; rb < 4; ++rb) acc[rb][0] = acc[rb][1] = q3::f32x4{0.f, 0.f, 0.f, 0.f};
+  auto to_mfma = [&](q3::u32x4 v) {
+    q3::u32x4 o;
+#pragma unroll
+    for (int e = 0; e < 4; ++e)
+      o[e] = static_cast<uint32_t>(__builtin_amdgcn_ds_bpermute(perm_addr, static_cast<int>(v[e])));
+    return o;
+  };
+#pragma unroll
+  for (int u = 0; u < kMaxSteps; ++u) {
+    if (u >= steps) break;
+    const q3::bf16x8 g = q3::as_bf16x8(to_mfma(bg[u]));
+    const q3::bf16x8 up = q3::as_bf16x8(to_mfma(bu[u]));
+    const int k = k0 + u * kKStep + kg;
+#pragma unroll
+    for (int rb = 0; rb < 4; ++rb) {
+      const q3::bf16x8 av =
+          q3::as_bf16x8(*reinterpret_cast<const q3::u32x4*>(a_s + (16 * rb + r16) * pitch + k));
+      acc[rb][0] = q3::mfma16x16x32(av, g, acc[rb][0]);
+      acc[rb][1] = q3::mfma16x16x32(av, up, acc[rb][1]);
+    }
+  }
+  __syncthreads();  // the rows are no longer read: their space takes the partial tiles
+  float* red = reinterpret_cast<float*>(a_s);  // [wave][rb][gate/up][4][64]
+#pragma unroll
+  for (int rb = 0; rb < 4; ++rb)
+#pragma unroll
+    for (int c = 0; c < 2; ++c)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) red[(((wave * 4 + rb) * 2 + c) * 4 + i) * 64 + lane] = acc[rb][c][i];
+  __syncthreads();
+  // wave rb < 4 finishes row block rb: sum the eight partials in wave order
+  if (wave >= 4) return;
+  const int rb = wave;
+  const int col = n0 + r16;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    float gsum = red[(((0 * 4 + rb) * 2 + 0) * 4 + i) * 64 + lane];
+    float usum = red[(((0 * 4 + rb) * 2 + 1) * 4 + i) * 64 + lane];
+#pragma unroll
+    for (int w = 1; w < kWaves64; ++w) {
+      gsum += red[(((w * 4 + rb) * 2 + 0) * 4 + i) * 64 + lane];
+      usum += red[(((w * 4 + rb) * 2 + 1) * 4 + i) * 64 + lane];
+    }
+    const int row = 16 * rb + 4 * (lane >> 4) + i;
+    if (row < a.M) {
+      const float g = round_bf16(gsum);
+      const float u = round_bf16(usum);
+      const float sg = round_bf16(g / (1.f + expf(-g)));
+      a.y[static_cast<int64_t>(row) * a.y_s + col] = to_bf16(sg * u);
+    }
+  }
+}
+
 // Embedding rows into the residual stream, with the per-16-column partial
 // sums of squares the first layer's norm needs.  One wave per row; an id
 // outside [0, vocab) gives a zero row.
@@ -337,6 +486,15 @@ extern "C" int qwen3_decode_linear_bf16(const void* x, int64_t x_row_stride, con
   a.up_row = up_row;
   q3::clear_error();
   auto s = static_cast<hipStream_t>(stream);
+  if (epilogue == kSilu && norm && M > 16 && K <= kMaxK64 && K % (kWaves64 * kKStep) == 0) {
+    // every row in one workgroup per column tile; the cross-wave partials
+    // (8 x 4 x 2 x 4 x 64 floats) reuse the rows' LDS
+    const size_t rows_lds = static_cast<size_t>(64) * (K + 8) * sizeof(uint16_t);
+    const size_t red_lds = static_cast<size_t>(kWaves64) * 4 * 2 * 4 * 64 * sizeof(float);
+    hipLaunchKernelGGL(gate_up64_kernel, dim3(static_cast<unsigned>(tiles)),
+                       dim3(kWaves64 * 64), rows_lds > red_lds ? rows_lds : red_lds, s, a);
+    return q3::launch_status(who);
+  }
   // (tile, row block) pairs, tiles rounded up to a multiple of the XCD count
   const int64_t blocks = q3::cdiv(tiles, kXcds) * kXcds * ((M + 15) / 16);
   // Eight waves (each an eighth of K) once K reaches 2048, so no wave runs

@@ -70,59 +70,9 @@ __global__ __launch_bounds__(kThreadsH) void lm_head_argmax_kernel(HeadArgs a) {
   const int pitch = a.K + 8;
   const int steps = a.K / kKStep;
 
-  // ---- rms of every row (four lanes per row, as the decode linears) ----
-  if (tid < 4 * kMaxRows) {
-    const int row = min(tid >> 2, a.M - 1);
-    const int part = tid & 3;
-    const float* sp = a.ss + static_cast<int64_t>(row) * a.ss_tiles;
-    float s = 0.f;
-    if (a.ss_tiles == 64) {
-      float4 f[4];
-#pragma unroll
-      for (int j = 0; j < 4; ++j) f[j] = reinterpret_cast<const float4*>(sp + 16 * part)[j];
-#pragma unroll
-      for (int j = 0; j < 4; ++j) s += ((f[j].x + f[j].y) + f[j].z) + f[j].w;
-    } else {
-      for (int t = part; t < a.ss_tiles; t += 4) s += sp[t];
-    }
-    s += __shfl_xor(s, 1, 64);
-    s += __shfl_xor(s, 2, 64);
-    if (part == 0) rms_s[tid >> 2] = 1.f / sqrtf(s / static_cast<float>(a.K) + a.eps);
-  }
-  __syncthreads();
-  // ---- stage a = bf16((h * rms) * w) for 64 rows (rows past M repeat M-1) ----
-  const int cpr = a.K >> 3;
-  for (int c = tid; c < kMaxRows * cpr; c += kThreadsH) {
-    const int r = c / cpr, cc = c - r * cpr;
-    const int row = min(r, a.M - 1);
-    const q3::u32x4 hv = q3::ld16(a.h + static_cast<int64_t>(row) * a.h_s + 8 * cc);
-    const q3::u32x4 nv = q3::ld16(a.norm_w + 8 * cc);
-    const float rr = rms_s[r];
-    q3::u32x4 o;
-#pragma unroll
-    for (int e = 0; e < 4; ++e)
-      o[e] = q3::pack_bf16x2((q3::bf16_lo(hv[e]) * rr) * q3::bf16_lo(nv[e]),
-                             (q3::bf16_hi(hv[e]) * rr) * q3::bf16_hi(nv[e]));
-    *reinterpret_cast<q3::u32x4*>(a_s + r * pitch + 8 * cc) = o;
-  }
-  __syncthreads();
-
-  // ---- vocabulary tiles ----
+  // The wave's first weight tile is requested before anything else: it does
+  // not depend on the rows.
   const int lrow = lane >> 2, lkg = 8 * (lane & 3);
-  const int perm_addr = 4 * (4 * r16 + (lane >> 4));
-  auto to_mfma = [&](q3::u32x4 v) {
-    q3::u32x4 o;
-#pragma unroll
-    for (int e = 0; e < 4; ++e)
-      o[e] = static_cast<uint32_t>(__builtin_amdgcn_ds_bpermute(perm_addr, static_cast<int>(v[e])));
-    return o;
-  };
-  unsigned long long best[kRowBlocks][4];
-#pragma unroll
-  for (int rb = 0; rb < kRowBlocks; ++rb)
-#pragma unroll
-    for (int i = 0; i < 4; ++i) best[rb][i] = 0ull;
-
   const int tiles = (a.V + 15) >> 4;
   const int stride = gridDim.x * kWavesH;
   // Weight row of this lane for tile t (rows past V repeat the last, masked
@@ -143,6 +93,77 @@ __global__ __launch_bounds__(kThreadsH) void lm_head_argmax_kernel(HeadArgs a) {
     load(bp, wrow, 0);
     load(bq, wrow, kC);
   }
+
+  // The rows of h, all loads in flight before the rms is known: chunk c =
+  // tid + i * threads of the 64 x K/8 16-byte chunks (at most 16 per thread
+  // for K <= 1024).  When the thread count is a multiple of the chunks per
+  // row, a thread's chunks share one column and so one norm-weight chunk.
+  constexpr int kChunksPerThread = 16;
+  const int cpr = a.K >> 3;
+  const int nch = kMaxRows * cpr;
+  const bool one_col = (kThreadsH) % cpr == 0;
+  q3::u32x4 hv[kChunksPerThread];
+  q3::u32x4 nv0 = {0u, 0u, 0u, 0u};
+  if (one_col) nv0 = q3::ld16(a.norm_w + 8 * (tid % cpr));
+#pragma unroll
+  for (int i = 0; i < kChunksPerThread; ++i) {
+    const int c = tid + i * (kThreadsH);
+    if (c >= nch) break;
+    const int r = c / cpr, cc = c - r * cpr;
+    hv[i] = q3::ld16(a.h + static_cast<int64_t>(min(r, a.M - 1)) * a.h_s + 8 * cc);
+  }
+  // ---- rms of every row (four lanes per row, as the decode linears) ----
+  if (tid < 4 * kMaxRows) {
+    const int row = min(tid >> 2, a.M - 1);
+    const int part = tid & 3;
+    const float* sp = a.ss + static_cast<int64_t>(row) * a.ss_tiles;
+    float s = 0.f;
+    if (a.ss_tiles == 64) {
+      float4 f[4];
+#pragma unroll
+      for (int j = 0; j < 4; ++j) f[j] = reinterpret_cast<const float4*>(sp + 16 * part)[j];
+#pragma unroll
+      for (int j = 0; j < 4; ++j) s += ((f[j].x + f[j].y) + f[j].z) + f[j].w;
+    } else {
+      for (int t = part; t < a.ss_tiles; t += 4) s += sp[t];
+    }
+    s += __shfl_xor(s, 1, 64);
+    s += __shfl_xor(s, 2, 64);
+    if (part == 0) rms_s[tid >> 2] = 1.f / sqrtf(s / static_cast<float>(a.K) + a.eps);
+  }
+  __syncthreads();
+  // a = bf16((h * rms) * w) for 64 rows (rows past M repeat M - 1)
+#pragma unroll
+  for (int i = 0; i < kChunksPerThread; ++i) {
+    const int c = tid + i * (kThreadsH);
+    if (c >= nch) break;
+    const int r = c / cpr, cc = c - r * cpr;
+    const q3::u32x4 nv = one_col ? nv0 : q3::ld16(a.norm_w + 8 * cc);
+    const float rr = rms_s[r];
+    q3::u32x4 o;
+#pragma unroll
+    for (int e = 0; e < 4; ++e)
+      o[e] = q3::pack_bf16x2((q3::bf16_lo(hv[i][e]) * rr) * q3::bf16_lo(nv[e]),
+                             (q3::bf16_hi(hv[i][e]) * rr) * q3::bf16_hi(nv[e]));
+    *reinterpret_cast<q3::u32x4*>(a_s + r * pitch + 8 * cc) = o;
+  }
+  __syncthreads();
+
+  // ---- vocabulary tiles ----
+  const int perm_addr = 4 * (4 * r16 + (lane >> 4));
+  auto to_mfma = [&](q3::u32x4 v) {
+    q3::u32x4 o;
+#pragma unroll
+    for (int e = 0; e < 4; ++e)
+      o[e] = static_cast<uint32_t>(__builtin_amdgcn_ds_bpermute(perm_addr, static_cast<int>(v[e])));
+    return o;
+  };
+  unsigned long long best[kRowBlocks][4];
+#pragma unroll
+  for (int rb = 0; rb < kRowBlocks; ++rb)
+#pragma unroll
+    for (int i = 0; i < 4; ++i) best[rb][i] = 0ull;
+
   for (; t < tiles; t += stride) {
     // The loads run one tile ahead: the last steps of a tile issue the
     // first steps of the wave's next tile, so the stream never drains.

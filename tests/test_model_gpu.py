@@ -171,6 +171,34 @@ def test_decode_linear_store_and_norm(gpu, M, K, N):
     _close(yn, refn, "norm prologue")
 
 
+@pytest.mark.parametrize("M", [17, 48, 64])
+def test_decode_linear_norm_silu_all_rows(gpu, M):
+    """SwiGLU linear with its RMSNorm prologue above 16 rows (every row in one
+    workgroup per column tile, the rows normalised once into LDS), against
+    y = bf16(bf16(silu(bf16 g)) * bf16 u) of the oracle norm; repeated calls
+    give the same bits."""
+    from qwen3_engine_from_scratch_amd.kernels.model_ops import decode_linear
+
+    announce(f"decode_linear norm + SwiGLU M={M}")
+    K, I = 1024, 3072
+    g = torch.Generator().manual_seed(M + 5)
+    x = (torch.randn(M, K, generator=g) * 2).to(torch.bfloat16)
+    wn = (1 + 0.1 * torch.randn(K, generator=g)).to(torch.bfloat16)
+    Wgu = (torch.randn(2 * I, K, generator=g) * 0.05).to(torch.bfloat16)
+    ss = (x.float() ** 2).view(M, K // 16, 16).sum(-1).contiguous()
+    args = dict(epilogue="silu", ss_in=ss.to(gpu), norm_weight=wn.to(gpu), eps=1e-6)
+    act = decode_linear(x.to(gpu), Wgu.to(gpu), **args)
+    a = oi.rms_norm(x, wn, 1e-6).float()
+    gg = (a @ Wgu[:I].float().T).to(torch.bfloat16).float()
+    uu = (a @ Wgu[I:].float().T).to(torch.bfloat16).float()
+    ref = (torch.nn.functional.silu(gg).to(torch.bfloat16).float() * uu).to(torch.bfloat16)
+    torch.cuda.synchronize()
+    _close(act, ref, "norm + SwiGLU")
+    again = decode_linear(x.to(gpu), Wgu.to(gpu), **args)
+    torch.cuda.synchronize()
+    assert torch.equal(again, act)
+
+
 def test_decode_linear_residual_and_silu_epilogues(gpu):
     from qwen3_engine_from_scratch_amd.kernels.model_ops import decode_linear, embed_ss
 
