@@ -40,12 +40,16 @@ constexpr int kD = 128;
 constexpr int kBN = 64;                   // keys per staged K/V tile
 constexpr int kRowBytes = kD * 2;         // one staged key row (256 B)
 constexpr int kTileElems = kBN * kD;      // one staged K or V tile (16 KiB)
-constexpr int kWaves = 4;
-constexpr int kDmaPerWave = kBN * kRowBytes / (kWaves * 64 * 16);  // 16-byte lanes
+// Workgroups of W = 4 or 8 waves (one or two per CU): eight waves share each
+// staged K/V tile among twice the query rows, halving the tile traffic per
+// flop, but hold items twice as large (fewer, coarser work items).
+template <int W>
+constexpr int dma_per_wave() { return kBN * kRowBytes / (W * 64 * 16); }  // 16-byte lanes
+constexpr int kMaxDma = 4;
 constexpr float kRescaleSlack = 8.f;      // log2 headroom before the max is raised
 constexpr int kMaxSeqs = 256;             // persistent path: sequences ranked in LDS
 constexpr int kScanMax = 1024;            // persistent path: query-tile ranks in LDS
-static_assert(kDmaPerWave == 4, "tile / workgroup shape");
+static_assert(dma_per_wave<4>() == kMaxDma && dma_per_wave<8>() == 2, "tile / workgroup shape");
 
 typedef __attribute__((address_space(3))) void lds_void_t;
 typedef short i16x4 __attribute__((__vector_size__(4 * sizeof(short))));
@@ -65,7 +69,7 @@ struct PrefillArgs {
   int64_t total;
   int Hq, G, HG;
   int groups;    // query-head groups (Hq / HG)
-  int rows;      // query rows per head per workgroup (32 * kWaves / HG)
+  int rows;      // query rows per head per workgroup (32 * W / HG)
   int n_mtiles;  // query tiles of the longest sequence
   float scale_log2;
   int causal;
@@ -81,20 +85,23 @@ struct TileBufs {
 
 // Per-lane byte offsets that do not change from tile to tile.
 struct LaneOffsets {
-  uint32_t kdma[kDmaPerWave];  // source offset of this lane's K chunk, load j
-  uint32_t vdma[kDmaPerWave];  // same for V
+  uint32_t kdma[kMaxDma];  // source offset of this lane's K chunk, load j
+  uint32_t vdma[kMaxDma];  // same for V
   uint32_t kread[8];           // LDS offset of the QK operand, d step t (key block 0)
   uint32_t vread[4];           // LDS offset of the PV operand, d block db (key chunk 0)
 };
 
+template <int W>
 __device__ __forceinline__ LaneOffsets lane_offsets(int lane, int wave, int64_t k_row_bytes,
                                                     int64_t v_row_bytes) {
   LaneOffsets o;
-  // Load j of wave w fills LDS block n = 4w + j (rows 4n .. 4n+3); lane i
-  // writes slot i % 16 of row 4n + i / 16, i.e. source chunk slot ^ swz(row).
+  // Load j of wave w fills LDS block n = D w + j (rows 4n .. 4n+3, D loads
+  // per wave); lane i writes slot i % 16 of row 4n + i / 16, i.e. source
+  // chunk slot ^ swz(row).
+  constexpr int D = dma_per_wave<W>();
 #pragma unroll
-  for (int j = 0; j < kDmaPerWave; ++j) {
-    const int row = 4 * (kDmaPerWave * wave + j) + (lane >> 4);
+  for (int j = 0; j < D; ++j) {
+    const int row = 4 * (D * wave + j) + (lane >> 4);
     const int slot = lane & 15;
     o.kdma[j] = static_cast<uint32_t>(row * k_row_bytes) + ((slot ^ (row & 15)) << 4);
     o.vdma[j] = static_cast<uint32_t>(row * v_row_bytes) + ((slot ^ (4 * (row & 3))) << 4);
@@ -117,6 +124,7 @@ __device__ __forceinline__ LaneOffsets lane_offsets(int lane, int wave, int64_t 
 }
 
 // Issues this wave's share of the loads of key tile n0 into (sk, sv).
+template <int W>
 __device__ __forceinline__ void tile_dma(const PrefillArgs& a, const LaneOffsets& off,
                                          int64_t start, int len, int kvh, int n0, uint16_t* sk,
                                          uint16_t* sv, int wave) {
@@ -130,9 +138,10 @@ __device__ __forceinline__ void tile_dma(const PrefillArgs& a, const LaneOffsets
       __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t*>(kb), 0, k_bytes, 0x00020000);
   const __amdgpu_buffer_rsrc_t vr =
       __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t*>(vb), 0, v_bytes, 0x00020000);
+  constexpr int D = dma_per_wave<W>();
 #pragma unroll
-  for (int j = 0; j < kDmaPerWave; ++j) {
-    const int blk = (kDmaPerWave * wave + j) * 512;  // elements: 1 KiB per load
+  for (int j = 0; j < D; ++j) {
+    const int blk = (D * wave + j) * 512;  // elements: 1 KiB per load
     __builtin_amdgcn_raw_ptr_buffer_load_lds(kr, (lds_void_t*)(sk + blk), 16, off.kdma[j], 0, 0, 0);
     __builtin_amdgcn_raw_ptr_buffer_load_lds(vr, (lds_void_t*)(sv + blk), 16, off.vdma[j], 0, 0, 0);
   }
@@ -220,6 +229,7 @@ __device__ __forceinline__ void wait_loads() {
 
 // One work item: query tile mt of sequence seq for head group hg.  Every
 // thread of the workgroup calls it.
+template <int W>
 __device__ __forceinline__ void prefill_item(const PrefillArgs& a, const LaneOffsets& off,
                                              int seq, int hg, int mt, const TileBufs& tb) {
   const int64_t start = a.cu[seq];
@@ -234,7 +244,7 @@ __device__ __forceinline__ void prefill_item(const PrefillArgs& a, const LaneOff
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // uniform: scalar branches
   const int l32 = lane & 31;
   const int hl = lane >> 5;
-  const int wph = kWaves / a.HG;  // waves per head
+  const int wph = W / a.HG;  // waves per head
   const int head = hg * a.HG + wave / wph;
   const int kvh = (hg * a.HG) / a.G;
   const int q0 = m0 + (wave % wph) * 32;  // first query row of this wave
@@ -243,7 +253,7 @@ __device__ __forceinline__ void prefill_item(const PrefillArgs& a, const LaneOff
   const int kend = a.causal ? min(len, m0 + a.rows) : len;
   const int n_tiles = (kend + kBN - 1) / kBN;
 
-  tile_dma(a, off, start, len, kvh, 0, tb.k0, tb.v0, wave);
+  tile_dma<W>(a, off, start, len, kvh, 0, tb.k0, tb.v0, wave);
 
   // Q^T as the B operand: lane (query l32, k-group hl), chunk c: dims
   // c*16 + 8*hl .. +7.
@@ -274,7 +284,7 @@ __device__ __forceinline__ void prefill_item(const PrefillArgs& a, const LaneOff
 
   auto tile = [&](int it, const uint16_t* kt, const uint16_t* vt, uint16_t* nk, uint16_t* nv) {
     const int n0 = it * kBN;
-    if (it + 1 < n_tiles) tile_dma(a, off, start, len, kvh, n0 + kBN, nk, nv, wave);
+    if (it + 1 < n_tiles) tile_dma<W>(a, off, start, len, kvh, n0 + kBN, nk, nv, wave);
 
     // Causal: the tile is entirely above this wave's last query row.
     const bool wave_skip = !wave_active || (a.causal && n0 > wave_last_q);
@@ -396,13 +406,14 @@ __device__ __forceinline__ void prefill_item(const PrefillArgs& a, const LaneOff
   __shared__ __attribute__((aligned(1024))) uint16_t s_k1[kTileElems]; \
   __shared__ __attribute__((aligned(1024))) uint16_t s_v1[kTileElems]; \
   const TileBufs tb{s_k0, s_v0, s_k1, s_v1};                           \
-  const LaneOffsets off = lane_offsets(threadIdx.x & 63, threadIdx.x >> 6, a.k_st * 2, a.v_st * 2)
+  const LaneOffsets off = lane_offsets<W>(threadIdx.x & 63, threadIdx.x >> 6, a.k_st * 2, a.v_st * 2)
 
 // Flat grid (fallback for many sequences / very long ones): one workgroup
 // per virtual item, head group fastest so consecutive workgroups go to
 // different XCDs and all items of one KV head share an XCD's L2; query tiles
 // heaviest first.  Items past a sequence's end exit at once.
-__global__ __launch_bounds__(kWaves * 64) __attribute__((amdgpu_waves_per_eu(2, 2)))
+template <int W>
+__global__ __launch_bounds__(W * 64) __attribute__((amdgpu_waves_per_eu(2, 2)))
 void varlen_prefill_flat_kernel(PrefillArgs a) {
   Q3_PREFILL_TILE_BUFFERS;
   const int64_t id = blockIdx.x;
@@ -410,13 +421,14 @@ void varlen_prefill_flat_kernel(PrefillArgs a) {
   const int seq = static_cast<int>((id / a.groups) % a.num_seqs);
   const int mt =
       a.n_mtiles - 1 - static_cast<int>(id / (static_cast<int64_t>(a.groups) * a.num_seqs));
-  prefill_item(a, off, seq, hg, mt, tb);
+  prefill_item<W>(a, off, seq, hg, mt, tb);
 }
 
 // Exclusive prefix sum over n <= kScanMax ints held in LDS (in place); returns
 // the total.  Called by all threads of the workgroup.
+template <int W>
 __device__ __forceinline__ int block_exclusive_scan(int* v, int n, int* s_wsum) {
-  constexpr int kPer = kScanMax / (kWaves * 64);
+  constexpr int kPer = kScanMax / (W * 64);
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   int local[kPer];
   int sum = 0;
@@ -436,7 +448,7 @@ __device__ __forceinline__ int block_exclusive_scan(int* v, int n, int* s_wsum) 
   __syncthreads();
   int run = incl - sum, total = 0;
 #pragma unroll
-  for (int w = 0; w < kWaves; ++w) {
+  for (int w = 0; w < W; ++w) {
     if (w < wave) run += s_wsum[w];
     total += s_wsum[w];
   }
@@ -459,26 +471,27 @@ __device__ __forceinline__ int block_exclusive_scan(int* v, int n, int* s_wsum) 
 #ifndef Q3_PREFILL_PERSISTENT_WAVES_PER_EU
 #define Q3_PREFILL_PERSISTENT_WAVES_PER_EU 2
 #endif
-__global__ __launch_bounds__(kWaves * 64)
+template <int W>
+__global__ __launch_bounds__(W * 64)
 __attribute__((amdgpu_waves_per_eu(Q3_PREFILL_PERSISTENT_WAVES_PER_EU, Q3_PREFILL_PERSISTENT_WAVES_PER_EU)))
 void varlen_prefill_persistent_kernel(PrefillArgs a) {
   Q3_PREFILL_TILE_BUFFERS;
   __shared__ int s_len[kMaxSeqs];
   __shared__ int s_sorted[kMaxSeqs];
   __shared__ int s_first[kScanMax];  // items before m-tile rank r (r = n_mtiles-1-mt)
-  __shared__ int s_wsum[kWaves];
+  __shared__ int s_wsum[W];
   const int tid = threadIdx.x;
   const int S = a.num_seqs;
   const int nm = a.n_mtiles;
 
-  for (int t = tid; t < S; t += kWaves * 64) {
+  for (int t = tid; t < S; t += W * 64) {
     const int64_t s0 = a.cu[t], s1 = a.cu[t + 1];
     const bool ok = s0 >= 0 && s1 <= a.total && s1 > s0;
     s_len[t] = ok ? static_cast<int>(s1 - s0) : 0;
   }
   __syncthreads();
   // Rank by length, longest first (ties by index).
-  for (int t = tid; t < S; t += kWaves * 64) {
+  for (int t = tid; t < S; t += W * 64) {
     const int lt = s_len[t];
     int rank = 0;
     for (int u = 0; u < S; ++u) {
@@ -489,7 +502,7 @@ void varlen_prefill_persistent_kernel(PrefillArgs a) {
   }
   __syncthreads();
   // Items of m-tile rank r: groups x (number of sequences longer than mt*rows).
-  for (int r = tid; r < nm; r += kWaves * 64) {
+  for (int r = tid; r < nm; r += W * 64) {
     const int mt = nm - 1 - r;
     const int64_t thr = static_cast<int64_t>(mt) * a.rows;
     int lo = 0, hi = S;  // first sorted index with len <= thr
@@ -500,13 +513,13 @@ void varlen_prefill_persistent_kernel(PrefillArgs a) {
     s_first[r] = lo * a.groups;
   }
   __syncthreads();
-  const int T = block_exclusive_scan(s_first, nm, s_wsum);
+  const int T = block_exclusive_scan<W>(s_first, nm, s_wsum);
 
-  const int W = gridDim.x;
+  const int nwg = gridDim.x;
   const int w = blockIdx.x;
-  const int w_mirror = (W / 8 - 1 - w / 8) * 8 + w % 8;
+  const int w_mirror = (nwg / 8 - 1 - w / 8) * 8 + w % 8;
   for (int round = 0;; ++round) {
-    const int64_t i = static_cast<int64_t>(round) * W + ((round & 1) ? w_mirror : w);
+    const int64_t i = static_cast<int64_t>(round) * nwg + ((round & 1) ? w_mirror : w);
     if (i >= T) break;
     int lo = 0, hi = nm - 1;  // largest rank r with s_first[r] <= i
     while (lo < hi) {
@@ -517,8 +530,37 @@ void varlen_prefill_persistent_kernel(PrefillArgs a) {
     const int seq = s_sorted[j / a.groups];
     const int hg = j % a.groups;
     __syncthreads();  // the previous item's LDS tiles are no longer read
-    prefill_item(a, off, seq, hg, nm - 1 - lo, tb);
+    prefill_item<W>(a, off, seq, hg, nm - 1 - lo, tb);
   }
+}
+
+// Sizes the items for W waves and launches the persistent grid (CUs x
+// resident workgroups, from the occupancy API) or, past its LDS tables, the
+// flat grid.
+template <int W>
+int launch_prefill(PrefillArgs a, int num_seqs, int max_seqlen, int cus, hipStream_t s,
+                   const char* who) {
+  a.rows = 32 * W / a.HG;
+  a.n_mtiles = static_cast<int>(q3::cdiv(max_seqlen, a.rows));
+  const int64_t blocks = static_cast<int64_t>(a.groups) * num_seqs * a.n_mtiles;
+  if (blocks > 0x7fffffff)
+    return q3::fail(QWEN3_EINVAL, "%s: grid too large (heads %d, seqs %d, max_seqlen %d)", who,
+                    a.Hq, num_seqs, max_seqlen);
+  int per_cu = 0;
+  const bool persistent =
+      num_seqs <= kMaxSeqs && a.n_mtiles <= kScanMax && cus > 0 &&
+      hipOccupancyMaxActiveBlocksPerMultiprocessor(
+          &per_cu, reinterpret_cast<const void*>(varlen_prefill_persistent_kernel<W>), W * 64,
+          0) == hipSuccess &&
+      per_cu > 0;
+  if (persistent) {
+    const int wgs = ((cus * per_cu + 7) / 8) * 8;  // multiple of 8 for the XCD-preserving snake
+    hipLaunchKernelGGL(varlen_prefill_persistent_kernel<W>, dim3(wgs), dim3(W * 64), 0, s, a);
+  } else {
+    hipLaunchKernelGGL(varlen_prefill_flat_kernel<W>, dim3(static_cast<unsigned>(blocks)),
+                       dim3(W * 64), 0, s, a);
+  }
+  return q3::launch_status(who);
 }
 
 }  // namespace
@@ -571,33 +613,23 @@ extern "C" int qwen3_varlen_prefill_bf16(const void* q, const int64_t q_strides[
   a.Hq = num_heads;
   a.G = num_heads / num_kv_heads;
   a.HG = a.G % 4 == 0 ? 4 : (a.G % 2 == 0 ? 2 : 1);
-  a.rows = 32 * kWaves / a.HG;
-  a.n_mtiles = static_cast<int>(q3::cdiv(max_seqlen, a.rows));
   a.scale_log2 = scale * q3::kLog2e;
   a.causal = causal ? 1 : 0;
   a.groups = num_heads / a.HG;
-  const int64_t blocks = static_cast<int64_t>(a.groups) * num_seqs * a.n_mtiles;
-  if (blocks > 0x7fffffff)
-    return q3::fail(QWEN3_EINVAL, "%s: grid too large (heads %d, seqs %d, max_seqlen %d)", who,
-                    num_heads, num_seqs, max_seqlen);
 
   q3::clear_error();
   hipStream_t s = static_cast<hipStream_t>(stream);
-  int dev = 0, cus = 0, per_cu = 0;
-  // The persistent grid is exactly what stays resident: CUs x workgroups per CU.
-  const bool persistent =
-      num_seqs <= kMaxSeqs && a.n_mtiles <= kScanMax && hipGetDevice(&dev) == hipSuccess &&
-      hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess &&
-      hipOccupancyMaxActiveBlocksPerMultiprocessor(
-          &per_cu, reinterpret_cast<const void*>(varlen_prefill_persistent_kernel), kWaves * 64,
-          0) == hipSuccess &&
-      cus > 0 && per_cu > 0;
-  if (persistent) {
-    const int wgs = ((cus * per_cu + 7) / 8) * 8;  // multiple of 8 for the XCD-preserving snake
-    hipLaunchKernelGGL(varlen_prefill_persistent_kernel, dim3(wgs), dim3(kWaves * 64), 0, s, a);
-  } else {
-    hipLaunchKernelGGL(varlen_prefill_flat_kernel, dim3(static_cast<unsigned>(blocks)),
-                       dim3(kWaves * 64), 0, s, a);
-  }
-  return q3::launch_status(who);
+  int dev = 0, cus = 0;
+  if (hipGetDevice(&dev) != hipSuccess ||
+      hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess)
+    cus = 0;
+  // Eight-wave workgroups once the batch holds enough of their (twice as
+  // large) work items to give every CU four: they halve the K/V tile
+  // traffic per flop, but a batch of a few short sequences needs the finer
+  // four-wave items to spread its causal work.
+  const int64_t rows8 = 32 * 8 / a.HG;
+  const int64_t items8 = static_cast<int64_t>(a.groups) * q3::cdiv(total_tokens, rows8);
+  const bool wide = cus > 0 && items8 >= 4 * static_cast<int64_t>(cus);
+  return wide ? launch_prefill<8>(a, num_seqs, max_seqlen, cus, s, who)
+              : launch_prefill<4>(a, num_seqs, max_seqlen, cus, s, who);
 }

@@ -55,23 +55,44 @@ def test_prefill_single_token_sequences_return_v(gpu):
             assert torch.equal(out[t, h], c.v[t, h // 2])
 
 
-def test_prefill_config2_vs_fp32(gpu):
-    """Qwen3-0.6B varlen prefill: 8 sequences, lengths uniform in [64, 2048]."""
-    c = oi.config2_prefill()
-    announce(f"prefill config2 lens={c.lens}")
-    out = _run(c, gpu, 16, 8)
+def _gpu_ref_fp32(c, gpu, G, causal=True):
+    """fp32 attention per sequence on the GPU (the closed form, GQA by
+    repeating each KV head G times)."""
     q, k, v = c.q.to(gpu), c.k.to(gpu), c.v.to(gpu)
     ref = torch.empty(q.shape, dtype=torch.float32, device=gpu)
     for s in range(len(c.lens)):
         s0, s1 = int(c.cu_seqlens[s]), int(c.cu_seqlens[s + 1])
         L = s1 - s0
         qs = q[s0:s1].float().transpose(0, 1).contiguous()
-        ks = k[s0:s1].float().transpose(0, 1).repeat_interleave(2, 0)
-        vs = v[s0:s1].float().transpose(0, 1).repeat_interleave(2, 0).contiguous()
+        ks = k[s0:s1].float().transpose(0, 1).repeat_interleave(G, 0)
+        vs = v[s0:s1].float().transpose(0, 1).repeat_interleave(G, 0).contiguous()
         sc = torch.matmul(qs, ks.transpose(1, 2).contiguous()) * c.scale
-        sc.masked_fill_(~torch.ones(L, L, dtype=torch.bool, device=gpu).tril(), float("-inf"))
+        if causal:
+            sc.masked_fill_(~torch.ones(L, L, dtype=torch.bool, device=gpu).tril(), float("-inf"))
         ref[s0:s1] = torch.matmul(torch.softmax(sc, -1), vs).transpose(0, 1)
-    assert_close_attn(out, ref.cpu(), "config2")
+    return ref.cpu()
+
+
+def test_prefill_config2_vs_fp32(gpu):
+    """Qwen3-0.6B varlen prefill: 8 sequences, lengths uniform in [64, 2048]."""
+    c = oi.config2_prefill()
+    announce(f"prefill config2 lens={c.lens}")
+    out = _run(c, gpu, 16, 8)
+    assert_close_attn(out, _gpu_ref_fp32(c, gpu, 2), "config2")
+
+
+@pytest.mark.parametrize("lens,hq,hkv,causal", [
+    ([4096, 3000, 5000, 4500], 16, 8, True),
+    ([2000, 7000], 32, 8, True),             # G = 4: 64-row items
+    ([4000, 4000, 4000, 4000], 16, 8, False),
+])
+def test_prefill_large_batches_vs_fp32(gpu, lens, hq, hkv, causal):
+    """Batches large enough for eight-wave workgroups (at least four of their
+    work items per CU)."""
+    c = oi.make_prefill_case(lens, hq, hkv, 128, seed=sum(lens) % 101)
+    announce(f"prefill large lens={lens} hq={hq} hkv={hkv} causal={causal}")
+    out = _run(c, gpu, hq, hkv, causal=causal)
+    assert_close_attn(out, _gpu_ref_fp32(c, gpu, hq // hkv, causal), f"lens={lens}")
 
 
 def test_prefill_batched_adaptor_pads_zero(gpu):
