@@ -197,8 +197,17 @@ int qwen3_kv_write_slots_bf16(const void* k_new, const int64_t k_new_strides[2],
  *   cu_seqlens int32 (num_seqs + 1,) on the device
  *   max_seqlen host-side upper bound of the sequence lengths (sizes the grid;
  *             the reference syncs cu_seqlens to the host to get it, :177-178)
+ *   workspace  optional (NULL: static schedule): qwen3_varlen_prefill_
+ *             workspace_bytes() bytes of device memory, zeroed before its
+ *             first use; every call leaves it zeroed.  With it a batch
+ *             large enough for eight-wave workgroups has its work items
+ *             dealt from counters as workgroups finish (heaviest first);
+ *             smaller batches keep the static order.  Concurrent calls
+ *             need separate workspaces.
  * Supported: head_dim 128, num_heads / num_kv_heads in [1, 16].
  * ---------------------------------------------------------------------- */
+size_t qwen3_varlen_prefill_workspace_bytes(void);
+
 int qwen3_varlen_prefill_bf16(const void* q, const int64_t q_strides[2],
                               const void* k, const int64_t k_strides[2],
                               const void* v, const int64_t v_strides[2],
@@ -206,7 +215,8 @@ int qwen3_varlen_prefill_bf16(const void* q, const int64_t q_strides[2],
                               const int32_t* cu_seqlens, int num_seqs,
                               int max_seqlen, int64_t total_tokens,
                               int num_heads, int num_kv_heads, int head_dim,
-                              float scale, int causal, void* stream);
+                              float scale, int causal, void* workspace,
+                              size_t workspace_bytes, void* stream);
 
 /* ------------------------------------------------------------------------
  * Fused pre-attention step: QK-RMSNorm + RoPE + K/V pool write.

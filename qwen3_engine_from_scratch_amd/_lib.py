@@ -51,11 +51,12 @@ _SIGNATURES = {
          _i64, _i, _vp, _i64,
          _i, _i, _i, _vp],
     ),
+    "qwen3_varlen_prefill_workspace_bytes": (ctypes.c_size_t, []),
     "qwen3_varlen_prefill_bf16": (
         _i,
         [_vp, _c_i64p, _vp, _c_i64p, _vp, _c_i64p, _vp, _c_i64p,
          _vp, _i, _i, _i64,
-         _i, _i, _i, ctypes.c_float, _i, _vp],
+         _i, _i, _i, ctypes.c_float, _i, _vp, ctypes.c_size_t, _vp],
     ),
     "qwen3_qk_norm_rope_decode_bf16": (
         _i,
@@ -101,7 +102,7 @@ _SIGNATURES = {
     ),
 }
 
-ABI_VERSION = 4
+ABI_VERSION = 5
 
 _lib = None
 

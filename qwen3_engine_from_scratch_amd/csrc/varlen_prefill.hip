@@ -49,6 +49,8 @@ constexpr int kMaxDma = 4;
 constexpr float kRescaleSlack = 8.f;      // log2 headroom before the max is raised
 constexpr int kMaxSeqs = 256;             // persistent path: sequences ranked in LDS
 constexpr int kScanMax = 1024;            // persistent path: query-tile ranks in LDS
+constexpr int kPools = 8;                 // dynamic schedule: one item pool per XCD
+constexpr int kPoolStride = 32;           // counters 128 bytes apart
 static_assert(dma_per_wave<4>() == kMaxDma && dma_per_wave<8>() == 2, "tile / workgroup shape");
 
 typedef __attribute__((address_space(3))) void lds_void_t;
@@ -73,6 +75,7 @@ struct PrefillArgs {
   int n_mtiles;  // query tiles of the longest sequence
   float scale_log2;
   int causal;
+  uint32_t* ctr;  // nullable: [32 p] next item of pool p, [32 kPools] workgroups done (zero between calls)
 };
 
 // The staged tiles of one workgroup: two K and two V buffers.
@@ -462,12 +465,19 @@ __device__ __forceinline__ int block_exclusive_scan(int* v, int n, int* s_wsum) 
   return total;
 }
 
-// Persistent grid (two workgroups per CU).  Every workgroup builds the same
-// compact list of non-empty items ordered heaviest first (query tiles of the
-// highest index first; within one, longest sequences first, head group
-// fastest) and takes its share in a snake order over rounds, which balances
-// the causal work per CU without atomics.  The snake mirrors whole groups of
-// 8 positions so an item's head group keeps mapping to the same XCD.
+// Persistent grid (CUs x resident workgroups).  Every workgroup builds the
+// same compact list of non-empty items ordered heaviest first (query tiles
+// of the highest index first; within one, longest sequences first, head
+// group fastest), and item i goes to XCD i % 8, so one head group's K/V
+// tiles stay in one XCD's L2.  Workgroup w takes item w first (the
+// heaviest items, one per workgroup).  With counters in the workspace (and
+// a multiple of 8 head groups) each XCD's workgroups then take that XCD's
+// remaining items from its pool as they finish -- longest-processing-time-
+// first list scheduling: a workgroup busy with a heavy item takes no more
+// until the others have theirs -- asking for the next one while the current
+// one runs, and take what other pools have left once theirs is empty.
+// Without them they take their share in a snake order over rounds
+// (mirroring whole groups of 8 positions so item i stays on XCD i % 8).
 #ifndef Q3_PREFILL_PERSISTENT_WAVES_PER_EU
 #define Q3_PREFILL_PERSISTENT_WAVES_PER_EU 2
 #endif
@@ -483,6 +493,14 @@ void varlen_prefill_persistent_kernel(PrefillArgs a) {
   const int tid = threadIdx.x;
   const int S = a.num_seqs;
   const int nm = a.n_mtiles;
+  // Workgroup 0 clears the counters before its first barrier (a workspace
+  // never used, or left mid-call, still gives every item to some workgroup:
+  // workgroup 0 takes items, from every pool, until all are done, and an
+  // item taken twice is computed twice with the same result).
+  if (a.ctr && blockIdx.x == 0 && tid <= kPools) {
+    const uint32_t prev = atomicExch(a.ctr + tid * kPoolStride, 0u);
+    asm volatile("" ::"v"(prev));  // performed before this thread reaches the barriers below
+  }
 
   for (int t = tid; t < S; t += W * 64) {
     const int64_t s0 = a.cu[t], s1 = a.cu[t + 1];
@@ -515,12 +533,7 @@ void varlen_prefill_persistent_kernel(PrefillArgs a) {
   __syncthreads();
   const int T = block_exclusive_scan<W>(s_first, nm, s_wsum);
 
-  const int nwg = gridDim.x;
-  const int w = blockIdx.x;
-  const int w_mirror = (nwg / 8 - 1 - w / 8) * 8 + w % 8;
-  for (int round = 0;; ++round) {
-    const int64_t i = static_cast<int64_t>(round) * nwg + ((round & 1) ? w_mirror : w);
-    if (i >= T) break;
+  auto run = [&](int64_t i) {
     int lo = 0, hi = nm - 1;  // largest rank r with s_first[r] <= i
     while (lo < hi) {
       const int mid = (lo + hi + 1) >> 1;
@@ -529,8 +542,71 @@ void varlen_prefill_persistent_kernel(PrefillArgs a) {
     const int j = static_cast<int>(i - s_first[lo]);
     const int seq = s_sorted[j / a.groups];
     const int hg = j % a.groups;
-    __syncthreads();  // the previous item's LDS tiles are no longer read
     prefill_item<W>(a, off, seq, hg, nm - 1 - lo, tb);
+  };
+  if (a.ctr && a.groups % kPools == 0 && gridDim.x % kPools == 0) {
+    // The first round is static (workgroup w takes item w: the heaviest
+    // items one per workgroup, spread over CUs as the snake spreads them);
+    // pool p holds the items after it with i % 8 == p: ticket j is item
+    // nwg + j * 8 + p.
+    const int64_t nwg = gridDim.x;
+    auto pool_items = [&](int q) -> int64_t {
+      return T > nwg + q ? (T - nwg - q + kPools - 1) / kPools : 0;
+    };
+    __shared__ int64_t s_item;
+    int pool = static_cast<int>(blockIdx.x % kPools);  // the XCD the dispatcher placed it on
+    uint32_t mine = 0;
+    if (tid == 0) mine = atomicAdd(a.ctr + pool * kPoolStride, 1u);
+    if (blockIdx.x < T) {
+      run(blockIdx.x);
+      __syncthreads();  // the item's LDS tiles are no longer read
+    }
+    for (;;) {
+      if (tid == 0) {
+        int64_t item = -1;
+        int64_t j = mine;
+        // an empty pool: read every pool's count (coherent loads) and ask
+        // the one with the most items left; a failed ask leaves that pool
+        // visibly empty, so this ends
+        while (j >= pool_items(pool)) {
+          int best_q = -1;
+          int64_t best = 0;
+          for (int q = 0; q < kPools; ++q) {
+            const int64_t left = pool_items(q) - static_cast<int64_t>(__hip_atomic_load(
+                a.ctr + q * kPoolStride, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT));
+            if (left > best) {
+              best = left;
+              best_q = q;
+            }
+          }
+          if (best_q < 0) break;
+          pool = best_q;
+          j = atomicAdd(a.ctr + pool * kPoolStride, 1u);
+        }
+        if (j < pool_items(pool)) item = nwg + j * kPools + pool;
+        s_item = item;
+      }
+      __syncthreads();  // also: the previous item's LDS tiles are no longer read
+      const int64_t i = s_item;
+      if (i < 0) break;
+      if (tid == 0) mine = atomicAdd(a.ctr + pool * kPoolStride, 1u);  // the next, one item ahead
+      run(i);
+      __syncthreads();  // every thread has read s_item
+    }
+    // the last workgroup to finish leaves every counter at zero
+    if (tid == 0 && atomicAdd(a.ctr + kPools * kPoolStride, 1u) == gridDim.x - 1) {
+      for (int q = 0; q <= kPools; ++q) atomicExch(a.ctr + q * kPoolStride, 0u);
+    }
+    return;
+  }
+  const int nwg = gridDim.x;
+  const int w = blockIdx.x;
+  const int w_mirror = (nwg / 8 - 1 - w / 8) * 8 + w % 8;
+  for (int round = 0;; ++round) {
+    const int64_t i = static_cast<int64_t>(round) * nwg + ((round & 1) ? w_mirror : w);
+    if (i >= T) break;
+    __syncthreads();  // the previous item's LDS tiles are no longer read
+    run(i);
   }
 }
 
@@ -565,13 +641,18 @@ int launch_prefill(PrefillArgs a, int num_seqs, int max_seqlen, int cus, hipStre
 
 }  // namespace
 
+extern "C" size_t qwen3_varlen_prefill_workspace_bytes(void) {
+  return (kPools + 1) * kPoolStride * sizeof(uint32_t);
+}
+
 extern "C" int qwen3_varlen_prefill_bf16(const void* q, const int64_t q_strides[2],
                                          const void* k, const int64_t k_strides[2],
                                          const void* v, const int64_t v_strides[2], void* o,
                                          const int64_t o_strides[2], const int32_t* cu_seqlens,
                                          int num_seqs, int max_seqlen, int64_t total_tokens,
                                          int num_heads, int num_kv_heads, int head_dim,
-                                         float scale, int causal, void* stream) {
+                                         float scale, int causal, void* workspace,
+                                         size_t workspace_bytes, void* stream) {
   const char* who = "qwen3_varlen_prefill_bf16";
   if (!q || !k || !v || !o || !cu_seqlens || !q_strides || !k_strides || !v_strides ||
       !o_strides)
@@ -616,6 +697,13 @@ extern "C" int qwen3_varlen_prefill_bf16(const void* q, const int64_t q_strides[
   a.scale_log2 = scale * q3::kLog2e;
   a.causal = causal ? 1 : 0;
   a.groups = num_heads / a.HG;
+  if (workspace) {
+    if (workspace_bytes < qwen3_varlen_prefill_workspace_bytes())
+      return q3::fail(QWEN3_EWORKSPACE, "%s: workspace of %zu bytes needed, %zu given", who,
+                      qwen3_varlen_prefill_workspace_bytes(), workspace_bytes);
+    if (!q3::aligned16(workspace))
+      return q3::fail(QWEN3_EALIGN, "%s: workspace must be 16-byte aligned", who);
+  }
 
   q3::clear_error();
   hipStream_t s = static_cast<hipStream_t>(stream);
@@ -630,6 +718,12 @@ extern "C" int qwen3_varlen_prefill_bf16(const void* q, const int64_t q_strides[
   const int64_t rows8 = 32 * 8 / a.HG;
   const int64_t items8 = static_cast<int64_t>(a.groups) * q3::cdiv(total_tokens, rows8);
   const bool wide = cus > 0 && items8 >= 4 * static_cast<int64_t>(cus);
+  // Items handed out from the counters only on the eight-wave path: with
+  // several rounds per workgroup the speed differences between CUs add up
+  // (measured: 8 x 4096 tokens 1125 -> 1045 us), while a batch of a few
+  // rounds is balanced better by the static snake (8 sequences of 64..2048
+  // tokens: 77 us static, 85 us from the counters).
+  if (workspace && wide) a.ctr = static_cast<uint32_t*>(workspace);
   return wide ? launch_prefill<8>(a, num_seqs, max_seqlen, cus, s, who)
               : launch_prefill<4>(a, num_seqs, max_seqlen, cus, s, who);
 }

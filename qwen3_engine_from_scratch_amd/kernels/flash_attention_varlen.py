@@ -13,11 +13,26 @@ from .. import _lib
 __all__ = ["flash_attention_prefill", "flash_attention_prefill_batched"]
 
 
+_WORKSPACES: dict = {}
+
+
+def _schedule_workspace(device, lib) -> torch.Tensor:
+    """The per-device zeroed counter buffer of the dynamic item schedule
+    (each call leaves it zeroed)."""
+    ws = _WORKSPACES.get(device)
+    if ws is None:
+        ws = torch.zeros(int(lib.qwen3_varlen_prefill_workspace_bytes()), dtype=torch.uint8,
+                         device=device)
+        _WORKSPACES[device] = ws
+    return ws
+
+
 def flash_attention_prefill(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
                             cu_seqlens: torch.Tensor, scale: float, num_heads: int,
                             num_kv_heads: int, head_dim: int, *,
                             max_seqlen: int | None = None, causal: bool = True,
-                            out: torch.Tensor | None = None) -> torch.Tensor:
+                            out: torch.Tensor | None = None,
+                            workspace: torch.Tensor | None = None) -> torch.Tensor:
     """Packed varlen prefill (reference: flash_attention_prefill,
     qwen3/kernels/flash_attention_varlen.py:126-194).
 
@@ -25,7 +40,10 @@ def flash_attention_prefill(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
     head_dim); cu_seqlens: int32 (num_seqs + 1,) cumulative lengths.
     Returns (total_tokens, num_heads, head_dim).  `max_seqlen` (host int) avoids
     the reference's device->host read of cu_seqlens (:177-178); when omitted
-    it is computed the same way the reference does.
+    it is computed the same way the reference does.  `workspace`: the
+    item counter of the dynamic schedule (default: one zeroed buffer per
+    device, kept by this module; concurrent calls on several streams pass
+    their own, zeroed once).
     """
     assert q.dim() == 3 and q.shape[1] == num_heads and q.shape[2] == head_dim
     assert k.shape == (q.shape[0], num_kv_heads, head_dim) and v.shape == k.shape
@@ -45,6 +63,8 @@ def flash_attention_prefill(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
     if out is None:
         out = torch.empty_like(q)
     lib = _lib.load()
+    if workspace is None:
+        workspace = _schedule_workspace(q.device, lib)
     rc = lib.qwen3_varlen_prefill_bf16(
         q.data_ptr(), _lib.strides(q, (0, 1)),
         k.data_ptr(), _lib.strides(k, (0, 1)),
@@ -52,7 +72,7 @@ def flash_attention_prefill(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
         out.data_ptr(), _lib.strides(out, (0, 1)),
         cu_seqlens.data_ptr(), num_seqs, int(max_seqlen), q.shape[0],
         num_heads, num_kv_heads, head_dim, float(scale), 1 if causal else 0,
-        _lib.stream_of(dev))
+        workspace.data_ptr(), workspace.numel(), _lib.stream_of(dev))
     _lib.check(rc, "qwen3_varlen_prefill_bf16")
     return out
 

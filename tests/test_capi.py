@@ -91,10 +91,13 @@ def test_prefill_rejects_bad_arguments():
     lib = _lib.load()
     s2 = _s(2048, 128)
 
-    def call(D=128, H=16, Hk=8, q=FAKE, qs=s2):
+    def call(D=128, H=16, Hk=8, q=FAKE, qs=s2, ws=None, wsb=0):
         return lib.qwen3_varlen_prefill_bf16(q, qs, FAKE, _s(1024, 128), FAKE, _s(1024, 128), FAKE, s2,
-                                             FAKE, 2, 100, 150, H, Hk, D, 0.088, 1, None)
+                                             FAKE, 2, 100, 150, H, Hk, D, 0.088, 1, ws, wsb, None)
 
+    need = lib.qwen3_varlen_prefill_workspace_bytes()
+    assert need == 9 * 128
+    assert call(ws=FAKE, wsb=need - 1) == -4  # a schedule workspace too small
     assert call(D=256) == -3
     assert call(H=12, Hk=8) == -3
     assert call(q=None) == -1

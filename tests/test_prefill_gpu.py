@@ -95,6 +95,41 @@ def test_prefill_large_batches_vs_fp32(gpu, lens, hq, hkv, causal):
     assert_close_attn(out, _gpu_ref_fp32(c, gpu, hq // hkv, causal), f"lens={lens}")
 
 
+def test_prefill_counter_schedule_matches_static(gpu):
+    """The item counters (a workspace) only reorder work: the output is the
+    same bits as the static order's, the counters end at zero, and a
+    workspace holding garbage gives the same result."""
+    from qwen3_engine_from_scratch_amd import _lib
+
+    lens, hq, hkv = [4000, 4000, 4000, 4000], 16, 8
+    c = oi.make_prefill_case(lens, hq, hkv, 128, seed=7)
+    q, k, v = c.q.to(gpu), c.k.to(gpu), c.v.to(gpu)
+    cu = c.cu_seqlens.to(gpu)
+    lib = _lib.load()
+    need = int(lib.qwen3_varlen_prefill_workspace_bytes())
+
+    def call(ws):
+        out = torch.empty_like(q)
+        rc = lib.qwen3_varlen_prefill_bf16(
+            q.data_ptr(), _lib.strides(q, (0, 1)), k.data_ptr(), _lib.strides(k, (0, 1)),
+            v.data_ptr(), _lib.strides(v, (0, 1)), out.data_ptr(), _lib.strides(out, (0, 1)),
+            cu.data_ptr(), len(lens), max(lens), q.shape[0], hq, hkv, 128, c.scale, 0,
+            None if ws is None else ws.data_ptr(), 0 if ws is None else ws.numel(),
+            _lib.stream_of(gpu))
+        _lib.check(rc, "qwen3_varlen_prefill_bf16")
+        torch.cuda.synchronize()
+        return out
+
+    announce(f"prefill counter schedule lens={lens}")
+    static = call(None)
+    ws = torch.zeros(need, dtype=torch.uint8, device=gpu)
+    for _ in range(2):
+        assert torch.equal(call(ws), static)
+        assert not ws.any(), "the counters were not left at zero"
+    ws.fill_(0xFF)
+    assert torch.equal(call(ws), static)
+
+
 def test_prefill_batched_adaptor_pads_zero(gpu):
     """flash_attention_prefill_batched on a right-padded batch: valid rows
     match the closed form, pad rows are zero (reference :252-258)."""
