@@ -544,69 +544,75 @@ void varlen_prefill_persistent_kernel(PrefillArgs a) {
     const int hg = j % a.groups;
     prefill_item<W>(a, off, seq, hg, nm - 1 - lo, tb);
   };
-  if (a.ctr && a.groups % kPools == 0 && gridDim.x % kPools == 0) {
-    // The first round is static (workgroup w takes item w: the heaviest
-    // items one per workgroup, spread over CUs as the snake spreads them);
-    // pool p holds the items after it with i % 8 == p: ticket j is item
-    // nwg + j * 8 + p.
-    const int64_t nwg = gridDim.x;
-    auto pool_items = [&](int q) -> int64_t {
-      return T > nwg + q ? (T - nwg - q + kPools - 1) / kPools : 0;
-    };
-    __shared__ int64_t s_item;
-    int pool = static_cast<int>(blockIdx.x % kPools);  // the XCD the dispatcher placed it on
-    uint32_t mine = 0;
-    if (tid == 0) mine = atomicAdd(a.ctr + pool * kPoolStride, 1u);
-    if (blockIdx.x < T) {
-      run(blockIdx.x);
+  // One loop and one inlined item body for both orders (each extra call
+  // site of `run` costs registers in the tile loop).
+  //  - static: round r takes item r * nwg + w, mirrored on odd rounds
+  //    (w' = the same XCD, the opposite end of the CU order), which pairs
+  //    heavy items with light ones;
+  //  - counters (eight-wave path, given a workspace): the first round is
+  //    the static one; pool p holds the later items with i % 8 == p
+  //    (ticket j is item nwg + j * 8 + p), a workgroup draws from the pool
+  //    of its XCD and, once that is empty, from the fullest pool.
+  const int64_t nwg = gridDim.x;
+  const int w = blockIdx.x;
+  const int w_mirror = (gridDim.x / 8 - 1 - w / 8) * 8 + w % 8;
+  const bool counters = a.ctr && a.groups % kPools == 0 && gridDim.x % kPools == 0;
+  auto pool_items = [&](int q) -> int64_t {
+    return T > nwg + q ? (T - nwg - q + kPools - 1) / kPools : 0;
+  };
+  __shared__ int64_t s_item;
+  int pool = static_cast<int>(blockIdx.x % kPools);  // the XCD the dispatcher placed it on
+  uint32_t mine = 0;                                  // thread 0: the next ticket, drawn ahead
+  // Counter order: the next item for the workgroup (every thread calls it).
+  auto draw = [&]() -> int64_t {
+    if (tid == 0) {
+      int64_t item = -1;
+      int64_t j = mine;
+      // an empty pool: read every pool's count (coherent loads) and ask the
+      // one with the most items left; a failed ask leaves that pool visibly
+      // empty, so this ends
+      while (j >= pool_items(pool)) {
+        int best_q = -1;
+        int64_t best = 0;
+        for (int q = 0; q < kPools; ++q) {
+          const int64_t left = pool_items(q) - static_cast<int64_t>(__hip_atomic_load(
+              a.ctr + q * kPoolStride, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT));
+          if (left > best) {
+            best = left;
+            best_q = q;
+          }
+        }
+        if (best_q < 0) break;
+        pool = best_q;
+        j = atomicAdd(a.ctr + pool * kPoolStride, 1u);
+      }
+      if (j < pool_items(pool)) {
+        item = nwg + j * kPools + pool;
+        mine = atomicAdd(a.ctr + pool * kPoolStride, 1u);  // the next, one item ahead
+      }
+      s_item = item;
+    }
+    __syncthreads();  // every thread has finished the previous item
+    const int64_t i = s_item;
+    __syncthreads();  // every thread has read s_item
+    return i;
+  };
+  if (counters && tid == 0) mine = atomicAdd(a.ctr + pool * kPoolStride, 1u);
+  int64_t i = w < T ? w : (counters ? draw() : -1);
+  for (int round = 1; i >= 0; ++round) {
+    run(i);
+    if (counters) {
+      i = draw();
+    } else {
+      i = static_cast<int64_t>(round) * nwg + ((round & 1) ? w_mirror : w);
+      if (i >= T) i = -1;
       __syncthreads();  // the item's LDS tiles are no longer read
     }
-    for (;;) {
-      if (tid == 0) {
-        int64_t item = -1;
-        int64_t j = mine;
-        // an empty pool: read every pool's count (coherent loads) and ask
-        // the one with the most items left; a failed ask leaves that pool
-        // visibly empty, so this ends
-        while (j >= pool_items(pool)) {
-          int best_q = -1;
-          int64_t best = 0;
-          for (int q = 0; q < kPools; ++q) {
-            const int64_t left = pool_items(q) - static_cast<int64_t>(__hip_atomic_load(
-                a.ctr + q * kPoolStride, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT));
-            if (left > best) {
-              best = left;
-              best_q = q;
-            }
-          }
-          if (best_q < 0) break;
-          pool = best_q;
-          j = atomicAdd(a.ctr + pool * kPoolStride, 1u);
-        }
-        if (j < pool_items(pool)) item = nwg + j * kPools + pool;
-        s_item = item;
-      }
-      __syncthreads();  // also: the previous item's LDS tiles are no longer read
-      const int64_t i = s_item;
-      if (i < 0) break;
-      if (tid == 0) mine = atomicAdd(a.ctr + pool * kPoolStride, 1u);  // the next, one item ahead
-      run(i);
-      __syncthreads();  // every thread has read s_item
-    }
-    // the last workgroup to finish leaves every counter at zero
-    if (tid == 0 && atomicAdd(a.ctr + kPools * kPoolStride, 1u) == gridDim.x - 1) {
-      for (int q = 0; q <= kPools; ++q) atomicExch(a.ctr + q * kPoolStride, 0u);
-    }
-    return;
   }
-  const int nwg = gridDim.x;
-  const int w = blockIdx.x;
-  const int w_mirror = (nwg / 8 - 1 - w / 8) * 8 + w % 8;
-  for (int round = 0;; ++round) {
-    const int64_t i = static_cast<int64_t>(round) * nwg + ((round & 1) ? w_mirror : w);
-    if (i >= T) break;
-    __syncthreads();  // the previous item's LDS tiles are no longer read
-    run(i);
+  if (counters && tid == 0 &&
+      atomicAdd(a.ctr + kPools * kPoolStride, 1u) == gridDim.x - 1) {
+    // the last workgroup to finish leaves every counter at zero
+    for (int q = 0; q <= kPools; ++q) atomicExch(a.ctr + q * kPoolStride, 0u);
   }
 }
 
@@ -718,11 +724,10 @@ extern "C" int qwen3_varlen_prefill_bf16(const void* q, const int64_t q_strides[
   const int64_t rows8 = 32 * 8 / a.HG;
   const int64_t items8 = static_cast<int64_t>(a.groups) * q3::cdiv(total_tokens, rows8);
   const bool wide = cus > 0 && items8 >= 4 * static_cast<int64_t>(cus);
-  // Items handed out from the counters only on the eight-wave path: with
-  // several rounds per workgroup the speed differences between CUs add up
-  // (measured: 8 x 4096 tokens 1125 -> 1045 us), while a batch of a few
-  // rounds is balanced better by the static snake (8 sequences of 64..2048
-  // tokens: 77 us static, 85 us from the counters).
+  // Items handed out from the counters only on the eight-wave path: over
+  // many rounds of mixed-length items they finish 1-2% sooner (64 prompts
+  // of 128..1024 tokens: 229 -> 224 us), while the few rounds of a small
+  // batch are paired better by the static snake.
   if (workspace && wide) a.ctr = static_cast<uint32_t*>(workspace);
   return wide ? launch_prefill<8>(a, num_seqs, max_seqlen, cus, s, who)
               : launch_prefill<4>(a, num_seqs, max_seqlen, cus, s, who);
