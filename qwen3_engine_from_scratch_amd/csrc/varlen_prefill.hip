@@ -316,12 +316,16 @@ __device__ __forceinline__ void prefill_item(const PrefillArgs& a, const LaneOff
       // ---- mask (diagonal / tail tiles only) and block max ----
       const bool need_mask = (n0 + kBN > len) || (a.causal && n0 + kBN - 1 > q0);
       if (need_mask) {
+        // score (kb, r) is key n0 + 4 hl + kr with kr = 32 kb + 8 (r / 4) +
+        // r % 4 (an inline constant): compare kr with per-lane limits
+        const int lim_len = len - n0 - 4 * hl;                   // kr < lim_len
+        const int lim_q = a.causal ? qrow - n0 - 4 * hl : kBN;  // kr <= lim_q
 #pragma unroll
         for (int kb = 0; kb < 2; ++kb)
 #pragma unroll
           for (int r = 0; r < 16; ++r) {
-            const int key = n0 + kb * 32 + 8 * (r / 4) + 4 * hl + (r % 4);
-            const bool valid = key < len && (!a.causal || key <= qrow);
+            const int kr = kb * 32 + 8 * (r / 4) + (r % 4);
+            const bool valid = kr < lim_len && kr <= lim_q;
             s[kb][r] = valid ? s[kb][r] : q3::kNegInf;
           }
       }
@@ -350,32 +354,38 @@ __device__ __forceinline__ void prefill_item(const PrefillArgs& a, const LaneOff
       for (int u = 0; u < kAhead; ++u) vf[u] = lds_vt(vt, pv_operand(off, u));
       __builtin_amdgcn_sched_barrier(0);
       const float m_use = m_run == q3::kNegInf ? 0.f : m_run;
-      // ---- P = exp2(s * c - m), P^T as B operands (chunk KC = 2 kb + kc) ----
-      q3::bf16x8 p[4];
-      float psum[4] = {0.f, 0.f, 0.f, 0.f};  // four independent sum chains
-#pragma unroll
-      for (int kb = 0; kb < 2; ++kb)
-#pragma unroll
-        for (int kc = 0; kc < 2; ++kc) {
-          float e[8];
-#pragma unroll
-          for (int i = 0; i < 8; ++i) {
-            e[i] = q3::fast_exp2(__builtin_fmaf(s[kb][8 * kc + i], c, -m_use));
-            psum[i & 3] += e[i];
-          }
-          q3::u32x4 pk = {q3::pack_bf16x2(e[0], e[1]), q3::pack_bf16x2(e[2], e[3]),
-                          q3::pack_bf16x2(e[4], e[5]), q3::pack_bf16x2(e[6], e[7])};
-          p[2 * kb + kc] = q3::as_bf16x8(pk);
+      // ---- P = exp2(s * c - m) as P^T B operands (chunk g = 2 kb + kc:
+      // scores s[kb][8 kc .. 8 kc + 7]) and O^T += V^T P^T, step u covering
+      // key chunk u / 4, dims 32 (u % 4) .. +31.  Chunk 0 is computed
+      // first; the exponentials of chunk g + 1 are issued between the four
+      // MFMAs of chunk g, two per step, so the VALU works while the matrix
+      // core runs.
+      q3::u32x4 pk[4];
+      float psum[4];  // four independent sum chains, started by chunk 0
+      auto exp_pair = [&](int g, int h) {  // scores 2h, 2h + 1 of chunk g
+        const int kb = g >> 1, kc = g & 1;
+        const float e0 = q3::fast_exp2(__builtin_fmaf(s[kb][8 * kc + 2 * h], c, -m_use));
+        const float e1 = q3::fast_exp2(__builtin_fmaf(s[kb][8 * kc + 2 * h + 1], c, -m_use));
+        if (g == 0 && h < 2) {
+          psum[2 * h] = e0;
+          psum[2 * h + 1] = e1;
+        } else {
+          psum[(2 * h) & 3] += e0;
+          psum[(2 * h + 1) & 3] += e1;
         }
-      l_run += (psum[0] + psum[1]) + (psum[2] + psum[3]);
+        pk[g][h] = q3::pack_bf16x2(e0, e1);
+      };
+#pragma unroll
+      for (int h = 0; h < 4; ++h) exp_pair(0, h);
       __builtin_amdgcn_sched_barrier(0);
-      // ---- O^T += V^T P^T: step u covers key chunk u / 4, dims 32 (u % 4) .. +31 ----
 #pragma unroll
       for (int u = 0; u < 16; ++u) {
-        acc[u & 3] = q3::mfma32x32x16(vf[u % kAhead], p[u >> 2], acc[u & 3]);
+        acc[u & 3] = q3::mfma32x32x16(vf[u % kAhead], q3::as_bf16x8(pk[u >> 2]), acc[u & 3]);
         if (u + kAhead < 16) vf[u % kAhead] = lds_vt(vt, pv_operand(off, u + kAhead));
+        if (u < 12) exp_pair((u >> 2) + 1, u & 3);
         __builtin_amdgcn_sched_barrier(0);
       }
+      l_run += (psum[0] + psum[1]) + (psum[2] + psum[3]);
     }
     wait_loads();
     __syncthreads();
@@ -533,14 +543,17 @@ void varlen_prefill_persistent_kernel(PrefillArgs a) {
   __syncthreads();
   const int T = block_exclusive_scan<W>(s_first, nm, s_wsum);
 
-  auto run = [&](int64_t i) {
+  // Item i (uniform, read from LDS): made scalar with readfirstlane so the
+  // item's indices and bounds live in SGPRs.
+  auto run = [&](int64_t i64) {
+    const int i = __builtin_amdgcn_readfirstlane(static_cast<int>(i64));
     int lo = 0, hi = nm - 1;  // largest rank r with s_first[r] <= i
     while (lo < hi) {
       const int mid = (lo + hi + 1) >> 1;
-      if (s_first[mid] <= i) lo = mid; else hi = mid - 1;
+      if (__builtin_amdgcn_readfirstlane(s_first[mid]) <= i) lo = mid; else hi = mid - 1;
     }
-    const int j = static_cast<int>(i - s_first[lo]);
-    const int seq = s_sorted[j / a.groups];
+    const int j = i - __builtin_amdgcn_readfirstlane(s_first[lo]);
+    const int seq = __builtin_amdgcn_readfirstlane(s_sorted[j / a.groups]);
     const int hg = j % a.groups;
     prefill_item<W>(a, off, seq, hg, nm - 1 - lo, tb);
   };
