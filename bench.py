@@ -77,24 +77,25 @@ def decode_bytes(lens, hq, hkv, head_dim=128, block_size=16):
 
 
 def time_steps(fn, steps, warmup):
-    """W untimed warmups, then K timed steps bracketed by synchronize; each
-    step is also bracketed by events on torch's current stream (where the
-    kernels are launched).  Returns (wall ms/step, mean event ms/step)."""
+    """W untimed warmups, then K timed steps bracketed by synchronize, and by
+    one pair of HIP events on torch's current stream (where the kernels are
+    launched) around the whole timed region.  Returns (wall ms/step, event
+    ms/step = region / K).  One event pair per step would add each event's
+    own cost to every step (about 6 us on a 70 us kernel)."""
     import torch
 
     for _ in range(warmup):
         fn()
     torch.cuda.synchronize()
-    ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
-          for _ in range(steps)]
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     t0 = time.perf_counter()
-    for s, e in ev:
-        s.record()
+    start.record()
+    for _ in range(steps):
         fn()
-        e.record()
+    end.record()
     torch.cuda.synchronize()
     wall = (time.perf_counter() - t0) * 1e3 / steps
-    evt = sum(s.elapsed_time(e) for s, e in ev) / steps
+    evt = start.elapsed_time(end) / steps
     return wall, evt
 
 

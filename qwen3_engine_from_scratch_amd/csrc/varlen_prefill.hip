@@ -633,21 +633,26 @@ void varlen_prefill_persistent_kernel(PrefillArgs a) {
 // resident workgroups, from the occupancy API) or, past its LDS tables, the
 // flat grid.
 template <int W>
-int launch_prefill(PrefillArgs a, int num_seqs, int max_seqlen, int cus, hipStream_t s,
-                   const char* who) {
+int launch_prefill(PrefillArgs a, int num_seqs, int max_seqlen, int dev, int cus,
+                   hipStream_t s, const char* who) {
   a.rows = 32 * W / a.HG;
   a.n_mtiles = static_cast<int>(q3::cdiv(max_seqlen, a.rows));
   const int64_t blocks = static_cast<int64_t>(a.groups) * num_seqs * a.n_mtiles;
   if (blocks > 0x7fffffff)
     return q3::fail(QWEN3_EINVAL, "%s: grid too large (heads %d, seqs %d, max_seqlen %d)", who,
                     a.Hq, num_seqs, max_seqlen);
-  int per_cu = 0;
-  const bool persistent =
-      num_seqs <= kMaxSeqs && a.n_mtiles <= kScanMax && cus > 0 &&
+  // Resident workgroups per CU, queried once per device (a host-side cost
+  // of every call otherwise).
+  static int occupancy[64] = {0};
+  int per_cu = dev >= 0 && dev < 64 ? occupancy[dev] : 0;
+  if (per_cu == 0 &&
       hipOccupancyMaxActiveBlocksPerMultiprocessor(
           &per_cu, reinterpret_cast<const void*>(varlen_prefill_persistent_kernel<W>), W * 64,
           0) == hipSuccess &&
-      per_cu > 0;
+      per_cu > 0 && dev >= 0 && dev < 64)
+    occupancy[dev] = per_cu;
+  const bool persistent =
+      num_seqs <= kMaxSeqs && a.n_mtiles <= kScanMax && cus > 0 && per_cu > 0;
   if (persistent) {
     const int wgs = ((cus * per_cu + 7) / 8) * 8;  // multiple of 8 for the XCD-preserving snake
     hipLaunchKernelGGL(varlen_prefill_persistent_kernel<W>, dim3(wgs), dim3(W * 64), 0, s, a);
@@ -726,10 +731,14 @@ extern "C" int qwen3_varlen_prefill_bf16(const void* q, const int64_t q_strides[
 
   q3::clear_error();
   hipStream_t s = static_cast<hipStream_t>(stream);
-  int dev = 0, cus = 0;
-  if (hipGetDevice(&dev) != hipSuccess ||
-      hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess)
-    cus = 0;
+  int dev = -1, cus = 0;
+  static int cu_cache[64] = {0};
+  if (hipGetDevice(&dev) == hipSuccess && dev >= 0 && dev < 64) {
+    cus = cu_cache[dev];
+    if (cus == 0 &&
+        hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess)
+      cu_cache[dev] = cus;
+  }
   // Eight-wave workgroups once the batch holds enough of their (twice as
   // large) work items to give every CU four: they halve the K/V tile
   // traffic per flop, but a batch of a few short sequences needs the finer
@@ -742,6 +751,6 @@ extern "C" int qwen3_varlen_prefill_bf16(const void* q, const int64_t q_strides[
   // of 128..1024 tokens: 229 -> 224 us), while the few rounds of a small
   // batch are paired better by the static snake.
   if (workspace && wide) a.ctr = static_cast<uint32_t*>(workspace);
-  return wide ? launch_prefill<8>(a, num_seqs, max_seqlen, cus, s, who)
-              : launch_prefill<4>(a, num_seqs, max_seqlen, cus, s, who);
+  return wide ? launch_prefill<8>(a, num_seqs, max_seqlen, dev, cus, s, who)
+              : launch_prefill<4>(a, num_seqs, max_seqlen, dev, cus, s, who);
 }
