@@ -95,6 +95,18 @@ def test_prefill_large_batches_vs_fp32(gpu, lens, hq, hkv, causal):
     assert_close_attn(out, _gpu_ref_fp32(c, gpu, hq // hkv, causal), f"lens={lens}")
 
 
+@pytest.mark.parametrize("n,lo,hi", [(260, 1, 40), (300, 1, 200)])
+def test_prefill_many_sequences_flat_grid(gpu, n, lo, hi):
+    """More sequences than the persistent kernel ranks in LDS (256): the flat
+    grid, with four-wave (few tokens) and eight-wave (many) workgroups."""
+    g = torch.Generator().manual_seed(n)
+    lens = [int(x) for x in torch.randint(lo, hi + 1, (n,), generator=g)]
+    c = oi.make_prefill_case(lens, 16, 8, 128, seed=n)
+    announce(f"prefill flat grid n={n} tokens={sum(lens)}")
+    out = _run(c, gpu, 16, 8)
+    assert_close_attn(out, _gpu_ref_fp32(c, gpu, 2), f"n={n}")
+
+
 def test_prefill_counter_schedule_matches_static(gpu):
     """The item counters (a workspace) only reorder work: the output is the
     same bits as the static order's, the counters end at zero, and a
