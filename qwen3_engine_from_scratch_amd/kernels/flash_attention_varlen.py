@@ -62,6 +62,10 @@ def flash_attention_prefill(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
         max_seqlen = int((cu_cpu[1:] - cu_cpu[:-1]).max().item()) if num_seqs > 0 else 0
     if out is None:
         out = torch.empty_like(q)
+    else:
+        assert out.shape == q.shape and out.dtype == torch.bfloat16 and out.stride(2) == 1, \
+            "out must be a bf16 (total_tokens, num_heads, head_dim) tensor with unit last stride"
+        _lib.require_hip(out)
     lib = _lib.load()
     if workspace is None:
         workspace = _schedule_workspace(q.device, lib)

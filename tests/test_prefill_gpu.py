@@ -95,6 +95,33 @@ def test_prefill_large_batches_vs_fp32(gpu, lens, hq, hkv, causal):
     assert_close_attn(out, _gpu_ref_fp32(c, gpu, hq // hkv, causal), f"lens={lens}")
 
 
+def test_prefill_strided_views_of_fused_qkv(gpu):
+    """q, k and v as head slices of one fused (T, 32, 128) projection (row
+    stride 4096 elements) and the output into a slice of a wider buffer: the
+    same bits as contiguous copies."""
+    from qwen3_engine_from_scratch_amd.kernels.flash_attention_varlen import flash_attention_prefill
+
+    lens = [300, 77, 1024, 5]
+    c = oi.make_prefill_case(lens, 16, 8, 128, seed=21)
+    T = sum(lens)
+    fused = torch.empty(T, 32, 128, dtype=torch.bfloat16, device=gpu)
+    fused[:, :16] = c.q.to(gpu)
+    fused[:, 16:24] = c.k.to(gpu)
+    fused[:, 24:] = c.v.to(gpu)
+    q, k, v = fused[:, :16], fused[:, 16:24], fused[:, 24:]
+    wide = torch.zeros(T, 20, 128, dtype=torch.bfloat16, device=gpu)
+    out = wide[:, 2:18]
+    cu = c.cu_seqlens.to(gpu)
+    announce("prefill strided views")
+    flash_attention_prefill(q, k, v, cu, c.scale, 16, 8, 128, max_seqlen=max(lens), out=out)
+    ref = flash_attention_prefill(q.contiguous(), k.contiguous(), v.contiguous(), cu, c.scale,
+                                  16, 8, 128, max_seqlen=max(lens))
+    torch.cuda.synchronize()
+    assert torch.equal(out, ref)
+    assert not wide[:, :2].any() and not wide[:, 18:].any()  # nothing outside the view
+    assert_close_attn(out.cpu(), _gpu_ref_fp32(c, gpu, 2), "strided")
+
+
 @pytest.mark.parametrize("n,lo,hi", [(260, 1, 40), (300, 1, 200)])
 def test_prefill_many_sequences_flat_grid(gpu, n, lo, hi):
     """More sequences than the persistent kernel ranks in LDS (256): the flat
