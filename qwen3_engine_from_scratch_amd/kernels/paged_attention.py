@@ -79,6 +79,10 @@ def paged_attention_decode_hip(q, k_buffer, v_buffer, block_table_2d,
         scale = 1.0 / math.sqrt(head_dim)
     if out is None:
         out = torch.empty_like(q)
+    else:
+        assert out.shape == q.shape and out.dtype == torch.bfloat16 and out.stride(2) == 1, \
+            "out must be a bf16 (B, num_heads, head_dim) tensor with unit last stride"
+        _lib.require_hip(out)
     max_rows, max_pages = block_table_2d.shape
     need = paged_decode_workspace_bytes(B, num_heads, head_dim, max_pages, block_size)
     if workspace is None or workspace.numel() < need:
