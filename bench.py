@@ -363,7 +363,7 @@ def bench_prefill(args, dev):
         rc = lib.qwen3_kv_write_slots_bf16(
             k.data_ptr(), _lib.strides(k, (0, 1)), v.data_ptr(), _lib.strides(v, (0, 1)),
             kb.data_ptr(), _lib.strides(kb, (0, 1, 2, 3)), vb.data_ptr(),
-            _lib.strides(vb, (0, 1, 2, 3)), nblk, 0, sm.data_ptr(), sm.numel(), 8, 128,
+            _lib.strides(vb, (0, 1, 2, 3)), nblk, 0, 1, sm.data_ptr(), sm.numel(), 8, 128,
             16, _lib.stream_of(dev))
         _lib.check(rc, "slots")
 

@@ -18,6 +18,9 @@
  *   - Out-of-range page ids, row ids and slots read from device tables are
  *     skipped by the kernels (never dereferenced), so a corrupt table cannot
  *     make a kernel read or write outside the buffers it was given.
+ *   - Entry points that write into the pool take its layer count
+ *     (num_layers) and reject layer_idx outside [0, num_layers) before
+ *     launching anything.
  *
  * Reference interfaces replaced (file:line in uphome/Qwen3-engine-from-scratch)
  *   qwen3_paged_decode_bf16    <- paged_attention_decode_triton
@@ -38,7 +41,7 @@
  *                              <- q_norm, k_norm, apply_rotary_pos_emb and the
  *                                 pool write that follows them
  *                                 (qwen3/attention.py:91-96, qwen3/norm.py:22-26,
- *                                 qwen3/rope.py:119-135 + the decode / prefill
+ *                                 qwen3/rope.py:88-110 + the decode / prefill
  *                                 writes above), fused into one launch
  */
 #ifndef QWEN3_ATTN_H
@@ -133,7 +136,7 @@ int qwen3_kv_write_decode_bf16(const void* k_new, const int64_t k_new_strides[2]
                                const void* v_new, const int64_t v_new_strides[2],
                                void* k_cache, const int64_t k_cache_strides[4],
                                void* v_cache, const int64_t v_cache_strides[4],
-                               int64_t num_blocks, int layer_idx,
+                               int64_t num_blocks, int layer_idx, int num_layers,
                                const int32_t* seq_lens,
                                const int32_t* block_table, int64_t bt_row_stride,
                                int64_t max_rows, int64_t max_pages,
@@ -159,7 +162,7 @@ int qwen3_kv_write_range_bf16(const void* k_new, const int64_t k_new_strides[2],
                               const void* v_new, const int64_t v_new_strides[2],
                               void* k_cache, const int64_t k_cache_strides[4],
                               void* v_cache, const int64_t v_cache_strides[4],
-                              int64_t num_blocks, int layer_idx,
+                              int64_t num_blocks, int layer_idx, int num_layers,
                               const int32_t* block_table_row, int64_t row_pages,
                               int64_t start_pos, int64_t num_tokens,
                               int num_kv_heads, int head_dim, int block_size,
@@ -179,7 +182,7 @@ int qwen3_kv_write_slots_bf16(const void* k_new, const int64_t k_new_strides[2],
                               const void* v_new, const int64_t v_new_strides[2],
                               void* k_cache, const int64_t k_cache_strides[4],
                               void* v_cache, const int64_t v_cache_strides[4],
-                              int64_t num_blocks, int layer_idx,
+                              int64_t num_blocks, int layer_idx, int num_layers,
                               const int64_t* slot_mapping, int64_t num_tokens,
                               int num_kv_heads, int head_dim, int block_size,
                               void* stream);
@@ -223,7 +226,7 @@ int qwen3_varlen_prefill_bf16(const void* q, const int64_t q_strides[2],
  *
  * Replaces, in one launch, q_norm / k_norm (qwen3/attention.py:91-92 with
  * qwen3/norm.py:22-26), apply_rotary_pos_emb (qwen3/attention.py:95-96,
- * qwen3/rope.py:119-135) and the pool write that follows
+ * qwen3/rope.py:88-110) and the pool write that follows
  * (update_kv_batch_triton, qwen3/kernels/paged_attention.py:292-377, for
  * decode; PagedKVCache.update, qwen3/PagedKVcache.py:177-214, for prefill).
  * Per head row: n = bf16((fp32(x) * rsqrt(mean(x^2) + eps)) * w);
@@ -258,7 +261,7 @@ int qwen3_qk_norm_rope_decode_bf16(const void* q, const int64_t q_strides[2],
                                    void* q_out, const int64_t q_out_strides[2],
                                    void* k_cache, const int64_t k_cache_strides[4],
                                    void* v_cache, const int64_t v_cache_strides[4],
-                                   int64_t num_blocks, int layer_idx,
+                                   int64_t num_blocks, int layer_idx, int num_layers,
                                    const int32_t* seq_lens, const int32_t* block_table,
                                    int64_t bt_row_stride, int64_t max_rows, int64_t max_pages,
                                    const int32_t* row_ids, const int64_t* positions, int B,
@@ -280,7 +283,8 @@ int qwen3_qk_norm_rope_slots_bf16(const void* q, const int64_t q_strides[2],
                                   void* k_out, const int64_t k_out_strides[2],
                                   void* k_cache, const int64_t k_cache_strides[4],
                                   void* v_cache, const int64_t v_cache_strides[4],
-                                  int64_t num_blocks, int layer_idx, int64_t num_tokens,
+                                  int64_t num_blocks, int layer_idx, int num_layers,
+                                  int64_t num_tokens,
                                   int num_heads, int num_kv_heads, int head_dim,
                                   int block_size, void* stream);
 

@@ -133,7 +133,7 @@ int qwen3_decode_qkv_rope_bf16(const void* h, int64_t h_row_stride,
                                void* q_out, const int64_t q_out_strides[2],
                                void* k_cache, const int64_t k_cache_strides[4],
                                void* v_cache, const int64_t v_cache_strides[4],
-                               int64_t num_blocks, int layer_idx,
+                               int64_t num_blocks, int layer_idx, int num_layers,
                                const int32_t* seq_lens, const int32_t* block_table,
                                int64_t bt_row_stride, int64_t max_rows, int64_t max_pages,
                                const int32_t* row_ids, int block_size, void* stream);

@@ -6,8 +6,8 @@ the same bytes on any machine with this torch build; tests fingerprint them
 
 QK-RMSNorm and RoPE restate the reference math used upstream of the kernels:
   rms_norm        qwen3/norm.py:22-26
-  rope_cos_sin    qwen3/rope.py:68-95   (cat(freqs, freqs) table, theta 1e6)
-  apply_rope      qwen3/rope.py:98-136  (rotate-half pairing i <-> i + D/2)
+  rope_cos_sin    qwen3/rope.py:49-69   (cat(freqs, freqs) table, theta 1e6)
+  apply_rope      qwen3/rope.py:72-110  (rotate-half pairing i <-> i + D/2)
 """
 from __future__ import annotations
 
@@ -26,7 +26,7 @@ def rms_norm(x: torch.Tensor, weight: torch.Tensor, eps: float = 1e-6) -> torch.
 
 
 def rope_cos_sin(positions: torch.Tensor, head_dim: int, base: float = 1e6):
-    """cos/sin tables gathered at `positions` (qwen3/rope.py:68-95)."""
+    """cos/sin tables gathered at `positions` (qwen3/rope.py:49-69)."""
     inv_freq = 1.0 / (base ** (torch.arange(0, head_dim, 2, dtype=torch.float32) / head_dim))
     freqs = positions.to(torch.float32)[..., None] * inv_freq
     emb = torch.cat((freqs, freqs), dim=-1)
@@ -40,7 +40,7 @@ def _rotate_half(x: torch.Tensor) -> torch.Tensor:
 
 def apply_rope(x: torch.Tensor, cos: torch.Tensor, sin: torch.Tensor) -> torch.Tensor:
     """x * cos + rotate_half(x) * sin with cos/sin cast to x.dtype
-    (qwen3/rope.py:132-135).  x: (..., T, H, D); cos/sin: (T, D)."""
+    (qwen3/rope.py:106-110).  x: (..., T, H, D); cos/sin: (T, D)."""
     c = cos[:, None, :].to(x.dtype)
     s = sin[:, None, :].to(x.dtype)
     return x * c + _rotate_half(x) * s

@@ -8,7 +8,7 @@ modules:
     input_layernorm (RMSNorm)     qwen3/norm.py:22-26
     qkv_proj, split into heads    qwen3/attention.py:81-88
     q_norm, k_norm                qwen3/attention.py:91-92
-    RoPE at positions 0..S-1      qwen3/rope.py:119-135, tables :53-68
+    RoPE at positions 0..S-1      qwen3/rope.py:88-110, tables :42-58
     causal GQA attention          qwen3/attention.py:193-207 (+ the causal
                                   mask of qwen3/model.py:150-161)
     o_proj, residual add          qwen3/attention.py:187, decoder.py:49

@@ -3,8 +3,8 @@
 TEST INFRASTRUCTURE ONLY (see oracle/__init__.py).  Restates, on the CPU in
 PyTorch, the reference's own modules in the order the attention layer calls
 them: RMSNorm (qwen3/norm.py:22-26) on q and k, then apply_rotary_pos_emb
-(qwen3/rope.py:119-135) with cos/sin gathered from the RotaryEmbedding
-tables (qwen3/rope.py:53-68, 70-79) at each token's position; the pool write
+(qwen3/rope.py:88-110) with cos/sin gathered from the RotaryEmbedding
+tables (qwen3/rope.py:42-58, 60-69) at each token's position; the pool write
 that follows is kv_write.slots_write_ref.
 """
 from __future__ import annotations
@@ -16,7 +16,7 @@ from .inputs import apply_rope, rms_norm
 
 def rope_tables(head_dim: int, base: float = 1e6, max_seq_len: int = 4096):
     """The model's fp32 cos/sin tables (max_seq_len, head_dim), built the way
-    RotaryEmbedding.__init__ builds them (qwen3/rope.py:53-68): inverse
+    RotaryEmbedding.__init__ builds them (qwen3/rope.py:42-58): inverse
     frequencies from even indices, an outer product over positions, and the
     frequencies repeated for both halves."""
     inv_freq = 1.0 / (base ** (torch.arange(0, head_dim, 2, dtype=torch.float32) / head_dim))

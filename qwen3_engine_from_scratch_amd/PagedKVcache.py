@@ -176,7 +176,7 @@ class PagedKVCache:
             v0.data_ptr(), _lib.strides(v0, (0, 1)),
             pool.k_buffer.data_ptr(), _lib.strides(pool.k_buffer, (0, 1, 2, 3)),
             pool.v_buffer.data_ptr(), _lib.strides(pool.v_buffer, (0, 1, 2, 3)),
-            pool.k_buffer.shape[0], int(layer_idx),
+            pool.k_buffer.shape[0], int(layer_idx), pool.k_buffer.shape[1],
             self.block_table_tensor.data_ptr(), self.num_pages,
             self.seq_len, S_new, pool.num_kv_heads, pool.head_dim, pool.block_size,
             _lib.stream_of(dev))
@@ -353,7 +353,7 @@ def write_prefill_batch(caches, layer_idx: int, k: torch.Tensor, v: torch.Tensor
         vt.data_ptr(), _lib.strides(vt, (0, 1)),
         pool.k_buffer.data_ptr(), _lib.strides(pool.k_buffer, (0, 1, 2, 3)),
         pool.v_buffer.data_ptr(), _lib.strides(pool.v_buffer, (0, 1, 2, 3)),
-        pool.k_buffer.shape[0], int(layer_idx),
+        pool.k_buffer.shape[0], int(layer_idx), pool.k_buffer.shape[1],
         slot_mapping.contiguous().data_ptr(), B * S,
         Hkv, D, pool.block_size, _lib.stream_of(dev))
     _lib.check(rc, "qwen3_kv_write_slots_bf16")

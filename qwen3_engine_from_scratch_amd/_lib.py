@@ -36,19 +36,19 @@ _SIGNATURES = {
     "qwen3_kv_write_decode_bf16": (
         _i,
         [_vp, _c_i64p, _vp, _c_i64p, _vp, _c_i64p, _vp, _c_i64p,
-         _i64, _i, _vp, _vp, _i64, _i64, _i64, _vp,
+         _i64, _i, _i, _vp, _vp, _i64, _i64, _i64, _vp,
          _i, _i, _i, _i, _vp],
     ),
     "qwen3_kv_write_range_bf16": (
         _i,
         [_vp, _c_i64p, _vp, _c_i64p, _vp, _c_i64p, _vp, _c_i64p,
-         _i64, _i, _vp, _i64, _i64, _i64,
+         _i64, _i, _i, _vp, _i64, _i64, _i64,
          _i, _i, _i, _vp],
     ),
     "qwen3_kv_write_slots_bf16": (
         _i,
         [_vp, _c_i64p, _vp, _c_i64p, _vp, _c_i64p, _vp, _c_i64p,
-         _i64, _i, _vp, _i64,
+         _i64, _i, _i, _vp, _i64,
          _i, _i, _i, _vp],
     ),
     "qwen3_varlen_prefill_workspace_bytes": (ctypes.c_size_t, []),
@@ -62,7 +62,7 @@ _SIGNATURES = {
         _i,
         [_vp, _c_i64p, _vp, _c_i64p, _vp, _c_i64p, _vp, _vp, ctypes.c_float,
          _vp, _vp, _i64, _i64,
-         _vp, _c_i64p, _vp, _c_i64p, _vp, _c_i64p, _i64, _i,
+         _vp, _c_i64p, _vp, _c_i64p, _vp, _c_i64p, _i64, _i, _i,
          _vp, _vp, _i64, _i64, _i64, _vp, _vp,
          _i, _i, _i, _i, _i, _vp],
     ),
@@ -70,7 +70,7 @@ _SIGNATURES = {
         _i,
         [_vp, _c_i64p, _vp, _c_i64p, _vp, _c_i64p, _vp, _vp, ctypes.c_float,
          _vp, _vp, _i64, _i64, _vp, _vp,
-         _vp, _c_i64p, _vp, _c_i64p, _vp, _c_i64p, _vp, _c_i64p, _i64, _i,
+         _vp, _c_i64p, _vp, _c_i64p, _vp, _c_i64p, _vp, _c_i64p, _i64, _i, _i,
          _i64, _i, _i, _i, _i, _vp],
     ),
     # include/qwen3_model_ops.h
@@ -97,12 +97,12 @@ _SIGNATURES = {
         _i,
         [_vp, _i64, _vp, _i, _vp, ctypes.c_float, _vp, _i64, _i, _i, _i, _i, _i,
          _vp, _vp, ctypes.c_float, _vp, _vp, _i64, _i64, _vp,
-         _vp, _c_i64p, _vp, _c_i64p, _vp, _c_i64p, _i64, _i,
+         _vp, _c_i64p, _vp, _c_i64p, _vp, _c_i64p, _i64, _i, _i,
          _vp, _vp, _i64, _i64, _i64, _vp, _i, _vp],
     ),
 }
 
-ABI_VERSION = 5
+ABI_VERSION = 6
 
 _lib = None
 

@@ -2,7 +2,7 @@
 // computes, for up to 64 tokens,
 //   qkv = RMSNorm(h) @ W_qkv^T                 (qwen3/attention.py:81, norm.py:22-26)
 //   q, k = RMSNorm_head(q), RMSNorm_head(k)    (qwen3/attention.py:91-92)
-//   q, k = RoPE(q, k) at each token's position (qwen3/rope.py:119-135)
+//   q, k = RoPE(q, k) at each token's position (qwen3/rope.py:88-110)
 // and stores q for the attention kernel and k, v into the paged pool at
 // position seq_lens[row] through the resident block table, as the decode
 // form of the pre-attention kernel does (qwen3/kernels/paged_attention.py:
@@ -330,6 +330,7 @@ extern "C" int qwen3_decode_qkv_rope_bf16(
     int64_t table_row_stride, int64_t table_rows, const int64_t* positions, void* q_out,
     const int64_t q_out_strides[2], void* k_cache, const int64_t k_cache_strides[4],
     void* v_cache, const int64_t v_cache_strides[4], int64_t num_blocks, int layer_idx,
+    int num_layers,
     const int32_t* seq_lens, const int32_t* block_table, int64_t bt_row_stride, int64_t max_rows,
     int64_t max_pages, const int32_t* row_ids, int block_size, void* stream) {
   const char* who = "qwen3_decode_qkv_rope_bf16";
@@ -342,6 +343,7 @@ extern "C" int qwen3_decode_qkv_rope_bf16(
                     head_dim, kD);
   if (M < 0 || M > kMaxRows || K <= 0 || num_heads <= 0 || num_kv_heads <= 0 ||
       ss_in_tiles <= 0 || block_size <= 0 || num_blocks <= 0 || layer_idx < 0 ||
+      layer_idx >= num_layers ||
       table_rows < 0 || max_rows <= 0 || max_pages <= 0 || bt_row_stride < max_pages ||
       !(eps >= 0.f) || !(head_eps >= 0.f))
     return q3::fail(QWEN3_EINVAL, "%s: bad sizes (M must be <= %d)", who, kMaxRows);

@@ -23,7 +23,7 @@ struct KvWriteArgs {
   uint16_t* v_cache;
   int64_t kc[4], vc[4];  // block, layer, head, slot strides
   int64_t num_blocks;
-  int layer;
+  int layer, num_layers;
   const int32_t* seq_lens;     // Decode
   const int32_t* block_table;  // Decode: full table; Range: one row
   int64_t bt_stride;           // Decode
@@ -93,11 +93,12 @@ __global__ __launch_bounds__(256) void kv_write_kernel(KvWriteArgs a) {
 int check_common(const KvWriteArgs& a, const char* who, bool* vec16) {
   if (!a.k_new || !a.v_new || !a.k_cache || !a.v_cache)
     return q3::fail(QWEN3_EINVAL, "%s: null tensor pointer", who);
-  if (a.H <= 0 || a.D <= 0 || a.bs <= 0 || a.num_blocks <= 0 || a.layer < 0)
+  if (a.H <= 0 || a.D <= 0 || a.bs <= 0 || a.num_blocks <= 0 || a.layer < 0 ||
+      a.layer >= a.num_layers)
     return q3::fail(QWEN3_EINVAL,
                     "%s: bad sizes (num_kv_heads=%d head_dim=%d block_size=%d "
-                    "num_blocks=%lld layer=%d)",
-                    who, a.H, a.D, a.bs, (long long)a.num_blocks, a.layer);
+                    "num_blocks=%lld layer=%d num_layers=%d)",
+                    who, a.H, a.D, a.bs, (long long)a.num_blocks, a.layer, a.num_layers);
   bool ok = a.D % 8 == 0 && q3::aligned16(a.k_new) && q3::aligned16(a.v_new) &&
             q3::aligned16(a.k_cache) && q3::aligned16(a.v_cache);
   const int64_t strides[] = {a.kn_s0, a.kn_s1, a.vn_s0, a.vn_s1, a.kc[0], a.kc[1],
@@ -149,6 +150,7 @@ extern "C" int qwen3_kv_write_decode_bf16(
     const void* k_new, const int64_t k_new_strides[2], const void* v_new,
     const int64_t v_new_strides[2], void* k_cache, const int64_t k_cache_strides[4],
     void* v_cache, const int64_t v_cache_strides[4], int64_t num_blocks, int layer_idx,
+    int num_layers,
     const int32_t* seq_lens, const int32_t* block_table, int64_t bt_row_stride,
     int64_t max_rows, int64_t max_pages, const int32_t* row_ids, int B, int num_kv_heads,
     int head_dim, int block_size, void* stream) {
@@ -168,6 +170,7 @@ extern "C" int qwen3_kv_write_decode_bf16(
              v_cache, v_cache_strides);
   a.num_blocks = num_blocks;
   a.layer = layer_idx;
+  a.num_layers = num_layers;
   a.seq_lens = seq_lens;
   a.block_table = block_table;
   a.bt_stride = bt_row_stride;
@@ -185,6 +188,7 @@ extern "C" int qwen3_kv_write_range_bf16(
     const void* k_new, const int64_t k_new_strides[2], const void* v_new,
     const int64_t v_new_strides[2], void* k_cache, const int64_t k_cache_strides[4],
     void* v_cache, const int64_t v_cache_strides[4], int64_t num_blocks, int layer_idx,
+    int num_layers,
     const int32_t* block_table_row, int64_t row_pages, int64_t start_pos,
     int64_t num_tokens, int num_kv_heads, int head_dim, int block_size, void* stream) {
   const char* who = "qwen3_kv_write_range_bf16";
@@ -204,6 +208,7 @@ extern "C" int qwen3_kv_write_range_bf16(
              v_cache, v_cache_strides);
   a.num_blocks = num_blocks;
   a.layer = layer_idx;
+  a.num_layers = num_layers;
   a.block_table = block_table_row;
   a.max_pages = row_pages;
   a.start_pos = start_pos;
@@ -218,6 +223,7 @@ extern "C" int qwen3_kv_write_slots_bf16(
     const void* k_new, const int64_t k_new_strides[2], const void* v_new,
     const int64_t v_new_strides[2], void* k_cache, const int64_t k_cache_strides[4],
     void* v_cache, const int64_t v_cache_strides[4], int64_t num_blocks, int layer_idx,
+    int num_layers,
     const int64_t* slot_mapping, int64_t num_tokens, int num_kv_heads, int head_dim,
     int block_size, void* stream) {
   const char* who = "qwen3_kv_write_slots_bf16";
@@ -230,6 +236,7 @@ extern "C" int qwen3_kv_write_slots_bf16(
              v_cache, v_cache_strides);
   a.num_blocks = num_blocks;
   a.layer = layer_idx;
+  a.num_layers = num_layers;
   a.slots = slot_mapping;
   a.n_items = num_tokens;
   a.H = num_kv_heads;

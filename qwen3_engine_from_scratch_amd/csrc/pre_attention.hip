@@ -5,9 +5,9 @@
 //
 // Arithmetic follows the reference step by step, with its roundings:
 //   RMSNorm (qwen3/norm.py:22-26):  n = bf16((fp32(x) * rsqrt(mean(x^2) + eps)) * w)
-//   RoPE (qwen3/rope.py:119-135):   c = bf16(cos[pos]), s = bf16(sin[pos]),
+//   RoPE (qwen3/rope.py:88-110):   c = bf16(cos[pos]), s = bf16(sin[pos]),
 //                                   out = bf16(bf16(n * c) + bf16(rotate_half(n) * s))
-//   rotate_half pairs element i with i + D/2 (qwen3/rope.py:82-85).
+//   rotate_half pairs element i with i + D/2 (qwen3/rope.py:72-85).
 // The cos/sin tables are the caller's (the model's fp32 tables), so no
 // transcendental is evaluated here.  Only the fp32 sum of squares may
 // associate differently from the reference's reduction, which can move a
@@ -49,7 +49,7 @@ struct PreAttnArgs {
   uint16_t* v_cache;
   int64_t kc[4], vc[4];
   int64_t num_blocks;
-  int layer;
+  int layer, num_layers;
   // Decode addressing: position and slot from the resident tables.
   const int32_t* seq_lens;
   const int32_t* block_table;
@@ -220,7 +220,7 @@ int check_args(const PreAttnArgs& a, int head_dim, const char* who) {
     return q3::fail(QWEN3_EUNSUPPORTED, "%s: head_dim %d not supported (built for %d)", who,
                     head_dim, kD);
   if (a.Hq <= 0 || a.Hkv <= 0 || a.bs <= 0 || a.num_blocks <= 0 || a.layer < 0 ||
-      a.tab_rows < 0 || a.n_tokens < 0 || !(a.eps >= 0.f))
+      a.layer >= a.num_layers || a.tab_rows < 0 || a.n_tokens < 0 || !(a.eps >= 0.f))
     return q3::fail(QWEN3_EINVAL, "%s: bad sizes", who);
   const void* ptrs[] = {a.q, a.k, a.v, a.q_w, a.k_w, a.cos_t, a.sin_t, a.q_out, a.k_cache,
                         a.v_cache};
@@ -259,7 +259,7 @@ void fill_common(PreAttnArgs& a, const void* q, const int64_t q_strides[2], cons
                  void* q_out, const int64_t q_out_strides[2], void* k_cache,
                  const int64_t k_cache_strides[4], void* v_cache,
                  const int64_t v_cache_strides[4], int64_t num_blocks, int layer_idx,
-                 int num_heads, int num_kv_heads, int block_size) {
+                 int num_layers, int num_heads, int num_kv_heads, int block_size) {
   a.q = static_cast<const uint16_t*>(q);
   a.q_s0 = q_strides[0];
   a.q_s1 = q_strides[1];
@@ -287,6 +287,7 @@ void fill_common(PreAttnArgs& a, const void* q, const int64_t q_strides[2], cons
   }
   a.num_blocks = num_blocks;
   a.layer = layer_idx;
+  a.num_layers = num_layers;
   a.Hq = num_heads;
   a.Hkv = num_kv_heads;
   a.bs = block_size;
@@ -300,7 +301,8 @@ extern "C" int qwen3_qk_norm_rope_decode_bf16(
     float eps, const float* cos_table, const float* sin_table, int64_t table_row_stride,
     int64_t table_rows, void* q_out, const int64_t q_out_strides[2], void* k_cache,
     const int64_t k_cache_strides[4], void* v_cache, const int64_t v_cache_strides[4],
-    int64_t num_blocks, int layer_idx, const int32_t* seq_lens, const int32_t* block_table,
+    int64_t num_blocks, int layer_idx, int num_layers, const int32_t* seq_lens,
+    const int32_t* block_table,
     int64_t bt_row_stride, int64_t max_rows, int64_t max_pages, const int32_t* row_ids,
     const int64_t* positions, int B, int num_heads, int num_kv_heads, int head_dim,
     int block_size, void* stream) {
@@ -313,8 +315,8 @@ extern "C" int qwen3_qk_norm_rope_decode_bf16(
   PreAttnArgs a{};
   fill_common(a, q, q_strides, k, k_strides, v, v_strides, q_weight, k_weight, eps, cos_table,
               sin_table, table_row_stride, table_rows, q_out, q_out_strides, k_cache,
-              k_cache_strides, v_cache, v_cache_strides, num_blocks, layer_idx, num_heads,
-              num_kv_heads, block_size);
+              k_cache_strides, v_cache, v_cache_strides, num_blocks, layer_idx, num_layers,
+              num_heads, num_kv_heads, block_size);
   a.seq_lens = seq_lens;
   a.block_table = block_table;
   a.bt_stride = bt_row_stride;
@@ -334,8 +336,8 @@ extern "C" int qwen3_qk_norm_rope_slots_bf16(
     int64_t table_rows, const int64_t* positions, const int64_t* slot_mapping, void* q_out,
     const int64_t q_out_strides[2], void* k_out, const int64_t k_out_strides[2], void* k_cache,
     const int64_t k_cache_strides[4], void* v_cache, const int64_t v_cache_strides[4],
-    int64_t num_blocks, int layer_idx, int64_t num_tokens, int num_heads, int num_kv_heads,
-    int head_dim, int block_size, void* stream) {
+    int64_t num_blocks, int layer_idx, int num_layers, int64_t num_tokens, int num_heads,
+    int num_kv_heads, int head_dim, int block_size, void* stream) {
   const char* who = "qwen3_qk_norm_rope_slots_bf16";
   if (!q_strides || !k_strides || !v_strides || !q_out_strides || !k_cache_strides ||
       !v_cache_strides || !positions || (k_out && !k_out_strides))
@@ -343,8 +345,8 @@ extern "C" int qwen3_qk_norm_rope_slots_bf16(
   PreAttnArgs a{};
   fill_common(a, q, q_strides, k, k_strides, v, v_strides, q_weight, k_weight, eps, cos_table,
               sin_table, table_row_stride, table_rows, q_out, q_out_strides, k_cache,
-              k_cache_strides, v_cache, v_cache_strides, num_blocks, layer_idx, num_heads,
-              num_kv_heads, block_size);
+              k_cache_strides, v_cache, v_cache_strides, num_blocks, layer_idx, num_layers,
+              num_heads, num_kv_heads, block_size);
   a.positions = positions;
   a.slots = slot_mapping;
   a.k_out = static_cast<uint16_t*>(k_out);

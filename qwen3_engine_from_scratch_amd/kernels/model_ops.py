@@ -266,7 +266,7 @@ def decode_qkv_rope(h: torch.Tensor, ss_in: torch.Tensor, norm_weight: torch.Ten
         cos_table.data_ptr(), sin_table.data_ptr(), cos_table.stride(0), cos_table.shape[0],
         _lib.ptr(positions), q_out.data_ptr(), _lib.strides(q_out, (0, 1)),
         kb.data_ptr(), _lib.strides(kb, (0, 1, 2, 3)), vb.data_ptr(), _lib.strides(vb, (0, 1, 2, 3)),
-        kb.shape[0], int(layer_idx), pool.seq_lens.data_ptr(), bt.data_ptr(), bt.stride(0),
+        kb.shape[0], int(layer_idx), kb.shape[1], pool.seq_lens.data_ptr(), bt.data_ptr(), bt.stride(0),
         bt.shape[0], bt.shape[1], _lib.ptr(row_ids), kb.shape[3], _lib.stream_of(dev))
     _lib.check(rc, "qwen3_decode_qkv_rope_bf16")
     return q_out

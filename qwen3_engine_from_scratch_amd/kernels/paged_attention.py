@@ -133,7 +133,7 @@ def update_kv_batch_hip(k_new, v_new, k_buffer, v_buffer, seq_lens,
         v_new.data_ptr(), _lib.strides(v_new, (0, 1)),
         k_buffer.data_ptr(), _lib.strides(k_buffer, (0, 1, 2, 3)),
         v_buffer.data_ptr(), _lib.strides(v_buffer, (0, 1, 2, 3)),
-        num_blocks, int(layer_idx),
+        num_blocks, int(layer_idx), num_layers,
         seq_lens.contiguous().data_ptr(),
         block_table_2d.data_ptr(), block_table_2d.stride(0), max_rows, max_pages,
         _lib.ptr(row_ids), B, num_kv_heads, head_dim, block_size, _lib.stream_of(dev))

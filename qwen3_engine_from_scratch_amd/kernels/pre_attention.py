@@ -7,7 +7,7 @@ apply_rotary_pos_emb; then update_kv_batch_triton for decode,
 qwen3/kernels/paged_attention.py:353-377, or PagedKVCache.update for
 prefill, qwen3/PagedKVcache.py:177-214).  The arithmetic, including its
 bf16 roundings, is the reference's (include/qwen3_attn.h states it); the
-RoPE tables are the model's own fp32 cos/sin tables (qwen3/rope.py:53-68).
+RoPE tables are the model's own fp32 cos/sin tables (qwen3/rope.py:42-58).
 """
 from __future__ import annotations
 
@@ -20,7 +20,7 @@ __all__ = ["qk_norm_rope_decode", "qk_norm_rope_prefill", "rope_tables"]
 
 def rope_tables(head_dim: int, base: float = 1e6, max_seq_len: int = 4096, device=None):
     """The model's fp32 cos/sin tables (max_seq_len, head_dim), as
-    RotaryEmbedding builds them (qwen3/rope.py:53-68): inverse frequencies
+    RotaryEmbedding builds them (qwen3/rope.py:42-58): inverse frequencies
     base^(-2i/head_dim), their outer product with the positions, repeated
     for both halves.  Computed on the CPU (like the reference's buffers) and
     moved to `device`."""
@@ -86,7 +86,7 @@ def qk_norm_rope_decode(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
         cos_table.stride(0), cos_table.shape[0],
         out.data_ptr(), _lib.strides(out, (0, 1)),
         kb.data_ptr(), _lib.strides(kb, (0, 1, 2, 3)), vb.data_ptr(), _lib.strides(vb, (0, 1, 2, 3)),
-        kb.shape[0], int(layer_idx), pool.seq_lens.data_ptr(), bt.data_ptr(), bt.stride(0),
+        kb.shape[0], int(layer_idx), kb.shape[1], pool.seq_lens.data_ptr(), bt.data_ptr(), bt.stride(0),
         bt.shape[0], bt.shape[1], _lib.ptr(row_ids), _lib.ptr(positions), B, Hq, Hkv, D,
         kb.shape[3],
         _lib.stream_of(dev))
@@ -129,6 +129,6 @@ def qk_norm_rope_prefill(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
         q_out.data_ptr(), _lib.strides(q_out, (0, 1)), k_out.data_ptr(), _lib.strides(k_out, (0, 1)),
         k_buffer.data_ptr(), _lib.strides(k_buffer, (0, 1, 2, 3)),
         v_buffer.data_ptr(), _lib.strides(v_buffer, (0, 1, 2, 3)),
-        k_buffer.shape[0], int(layer_idx), T, Hq, Hkv, D, k_buffer.shape[3], _lib.stream_of(dev))
+        k_buffer.shape[0], int(layer_idx), k_buffer.shape[1], T, Hq, Hkv, D, k_buffer.shape[3], _lib.stream_of(dev))
     _lib.check(rc, "qwen3_qk_norm_rope_slots_bf16")
     return q_out, k_out

@@ -54,7 +54,7 @@ class RMSNorm(nn.Module):
 
 
 class RotaryEmbedding(nn.Module):
-    """fp32 cos/sin tables (max_seq_len, head_dim) (qwen3/rope.py:41-57).
+    """fp32 cos/sin tables (max_seq_len, head_dim) (qwen3/rope.py:42-58).
     Kept as plain fp32 tensors, not buffers, so casting the model to bf16
     leaves them alone: the kernels round cos/sin to bf16 themselves, as the
     reference's cast to q.dtype does."""

@@ -108,11 +108,11 @@ def test_pre_attention_rejects_bad_arguments():
     lib = _lib.load()
     qs, ks, c4 = _s(4096, 128), _s(4096, 128), _s(1 << 16, 1 << 14, 2048, 128)
 
-    def dec(D=128, q=FAKE, q_strides=qs, tab_stride=128, bt_stride=8):
+    def dec(D=128, q=FAKE, q_strides=qs, tab_stride=128, bt_stride=8, layer=0, layers=4):
         return lib.qwen3_qk_norm_rope_decode_bf16(
             q, q_strides, FAKE, ks, FAKE, ks, FAKE, FAKE, 1e-6, FAKE, FAKE, tab_stride, 64,
-            FAKE, _s(2048, 128), FAKE, c4, FAKE, c4, 16, 0, FAKE, FAKE, bt_stride, 4, 8, None,
-            None, 2, 16, 8, D, 16, None)
+            FAKE, _s(2048, 128), FAKE, c4, FAKE, c4, 16, layer, layers, FAKE, FAKE, bt_stride,
+            4, 8, None, None, 2, 16, 8, D, 16, None)
 
     assert dec(D=64) == -3
     assert dec(q=None) == -1
@@ -120,14 +120,17 @@ def test_pre_attention_rejects_bad_arguments():
     assert dec(q_strides=_s(4100, 128)) == -2
     assert dec(tab_stride=130) == -2
     assert dec(bt_stride=4) == -1  # table rows shorter than max_pages
+    assert dec(layer=4) == -1 and dec(layer=-1) == -1  # layer outside the pool
 
-    def slots(positions=FAKE, D=128):
+    def slots(positions=FAKE, D=128, layer=0):
         return lib.qwen3_qk_norm_rope_slots_bf16(
             FAKE, qs, FAKE, ks, FAKE, ks, FAKE, FAKE, 1e-6, FAKE, FAKE, 128, 64, positions, None,
-            FAKE, _s(2048, 128), None, None, FAKE, c4, FAKE, c4, 16, 0, 5, 16, 8, D, 16, None)
+            FAKE, _s(2048, 128), None, None, FAKE, c4, FAKE, c4, 16, layer, 2, 5, 16, 8, D, 16,
+            None)
 
     assert slots(positions=None) == -1
     assert slots(D=256) == -3
+    assert slots(layer=2) == -1
 
 
 def test_model_ops_reject_bad_arguments():
@@ -165,14 +168,15 @@ def test_model_ops_reject_bad_arguments():
     assert lib.qwen3_page_in_bf16(FAKE, 16, 4, 16, FAKE, 2, FAKE, FAKE, 100, 10, None) == -2  # odd block
     s2, s4 = _s(2048, 128), _s(1 << 16, 1 << 14, 2048, 128)
 
-    def qkv(M=16, K=1024, D=128, ss=FAKE, bt_stride=8):
+    def qkv(M=16, K=1024, D=128, ss=FAKE, bt_stride=8, layer=0):
         return lib.qwen3_decode_qkv_rope_bf16(
             FAKE, K, ss, 64, FAKE, 1e-6, FAKE, K, M, K, 16, 8, D, FAKE, FAKE, 1e-6, FAKE, FAKE,
-            128, 64, None, FAKE, s2, FAKE, s4, FAKE, s4, 16, 0, FAKE, FAKE, bt_stride, 4, 8,
-            None, 16, None)
+            128, 64, None, FAKE, s2, FAKE, s4, FAKE, s4, 16, layer, 28, FAKE, FAKE, bt_stride,
+            4, 8, None, 16, None)
 
     assert qkv(M=65) == -1 and qkv(D=64) == -3 and qkv(K=1000) == -3 and qkv(K=4160) == -3
     assert qkv(ss=None) == -1 and qkv(bt_stride=4) == -1
+    assert qkv(layer=28) == -1
     ws = lib.qwen3_lm_head_argmax_workspace_bytes()
     assert ws > 0
 
@@ -191,12 +195,26 @@ def test_model_ops_reject_bad_arguments():
 def test_kv_write_rejects_bad_arguments():
     lib = _lib.load()
     c4 = _s(1 << 16, 1 << 14, 2048, 128)
-    rc = lib.qwen3_kv_write_range_bf16(FAKE, _s(1024, 128), FAKE, _s(1024, 128), FAKE, c4, FAKE, c4,
-                                       64, 0, FAKE, 2, 20, 40, 8, 128, 16, None)
-    assert rc == -1  # positions 20..59 need 4 pages, the row has 2
-    rc = lib.qwen3_kv_write_decode_bf16(FAKE, _s(1024, 128), FAKE, _s(1024, 128), FAKE, c4, FAKE, c4,
-                                        64, 0, None, FAKE, 8, 4, 8, None, 2, 8, 128, 16, None)
-    assert rc == -1  # null seq_lens
+    n = _s(1024, 128)
+
+    def rng(layer=0, layers=1, start=20):
+        return lib.qwen3_kv_write_range_bf16(FAKE, n, FAKE, n, FAKE, c4, FAKE, c4, 64, layer,
+                                             layers, FAKE, 2, start, 40, 8, 128, 16, None)
+
+    assert rng() == -1  # positions 20..59 need 4 pages, the row has 2
+    assert rng(start=0, layer=1, layers=1) == -1  # layer outside the pool
+    assert rng(start=0, layer=-1, layers=4) == -1
+
+    def dec(sl=FAKE, layer=0, layers=4):
+        return lib.qwen3_kv_write_decode_bf16(FAKE, n, FAKE, n, FAKE, c4, FAKE, c4, 64, layer,
+                                              layers, sl, FAKE, 8, 4, 8, None, 2, 8, 128, 16,
+                                              None)
+
+    assert dec(sl=None) == -1  # null seq_lens
+    assert dec(layer=4) == -1 and dec(layer=7, layers=4) == -1
+    slot = lambda layer, layers: lib.qwen3_kv_write_slots_bf16(  # noqa: E731
+        FAKE, n, FAKE, n, FAKE, c4, FAKE, c4, 64, layer, layers, FAKE, 10, 8, 128, 16, None)
+    assert slot(2, 2) == -1 and slot(0, 0) == -1
 
 
 def test_wrappers_refuse_cpu_tensors():

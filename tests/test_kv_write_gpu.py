@@ -90,7 +90,7 @@ def test_slots_write_with_padding(gpu):
     rc = _lib.load().qwen3_kv_write_slots_bf16(
         k_new.data_ptr(), _lib.strides(k_new, (0, 1)), v_new.data_ptr(), _lib.strides(v_new, (0, 1)),
         kb.data_ptr(), _lib.strides(kb, (0, 1, 2, 3)), vb.data_ptr(), _lib.strides(vb, (0, 1, 2, 3)),
-        nb, 1, sm.data_ptr(), T, Hkv, D, bs, _lib.stream_of(gpu))
+        nb, 1, layers, sm.data_ptr(), T, Hkv, D, bs, _lib.stream_of(gpu))
     _lib.check(rc, "slots")
     torch.cuda.synchronize()
     assert np.array_equal(_u16(kb), ek) and np.array_equal(_u16(vb), ev)
@@ -159,7 +159,7 @@ def test_slot_write_golden_fixture(gpu):
     rc = _lib.load().qwen3_kv_write_slots_bf16(
         k.data_ptr(), _lib.strides(k, (0, 1)), v.data_ptr(), _lib.strides(v, (0, 1)),
         kb.data_ptr(), _lib.strides(kb, (0, 1, 2, 3)), vb.data_ptr(), _lib.strides(vb, (0, 1, 2, 3)),
-        kb.shape[0], 1, sm.data_ptr(), sm.numel(), 8, 128, 16, _lib.stream_of(gpu))
+        kb.shape[0], 1, kb.shape[1], sm.data_ptr(), sm.numel(), 8, 128, 16, _lib.stream_of(gpu))
     _lib.check(rc, "slots")
     torch.cuda.synchronize()
     ku, vu = _u16(kb), _u16(vb)
