@@ -4,6 +4,7 @@ import pytest
 import torch
 
 from conftest import announce
+from oracle import inputs as oi
 from oracle import kv_write as ok
 
 pytestmark = pytest.mark.gpu
@@ -166,3 +167,39 @@ def test_slot_write_golden_fixture(gpu):
     assert np.uint64(ku.astype(np.uint64).sum()) == f["k_checksum"]
     assert np.uint64(vu.astype(np.uint64).sum()) == f["v_checksum"]
     assert np.array_equal(np.argwhere(ku.any(axis=(2, 4))), f["touched"])
+
+
+def test_config2_slot_write_full_size_bit_exact(gpu):
+    """The Qwen3-0.6B prefill workload's slot write at its own size: 8
+    sequences, 8,115 tokens, the seeded slot mapping through a permuted pool,
+    into layer 1 of a 2-layer pool; the whole pool compared with the oracle
+    (every written slot bit-exact, every other slot still zero)."""
+    from qwen3_engine_from_scratch_amd import _lib
+
+    c = oi.config2_prefill()
+    T = int(c.cu_seqlens[-1])
+    assert T == sum(c.lens) == 8115
+    nb = c.num_blocks + 7  # a few blocks no sequence owns
+    kb = torch.zeros(nb, 2, 8, 16, 128, dtype=torch.bfloat16, device=gpu)
+    vb = torch.zeros_like(kb)
+    ek = np.zeros(tuple(kb.shape), np.uint16)
+    ev = np.zeros_like(ek)
+    ok.slots_write_ref(_u16(c.k), _u16(c.v), ek, ev, c.slot_mapping.numpy(), 1)
+    k, v, sm = c.k.to(gpu), c.v.to(gpu), c.slot_mapping.to(gpu)
+    announce(f"config2 slot write T={T} lens={c.lens}")
+    rc = _lib.load().qwen3_kv_write_slots_bf16(
+        k.data_ptr(), _lib.strides(k, (0, 1)), v.data_ptr(), _lib.strides(v, (0, 1)),
+        kb.data_ptr(), _lib.strides(kb, (0, 1, 2, 3)), vb.data_ptr(), _lib.strides(vb, (0, 1, 2, 3)),
+        nb, 1, 2, sm.data_ptr(), T, 8, 128, 16, _lib.stream_of(gpu))
+    _lib.check(rc, "slots")
+    torch.cuda.synchronize()
+    ku, vu = _u16(kb), _u16(vb)
+    assert np.array_equal(ku, ek) and np.array_equal(vu, ev)
+    # independent read path: each sequence gathered back through its pages
+    cu = c.cu_seqlens.tolist()
+    bs = 16
+    for s, L in enumerate(c.lens):
+        sl = c.slot_mapping[cu[s]:cu[s + 1]].numpy()
+        table = sl[::bs] // bs
+        got = ok.gather_tokens(ku, 1, table, L)  # (Hkv, L, D)
+        assert np.array_equal(got, _u16(c.k[cu[s]:cu[s + 1]]).transpose(1, 0, 2))
