@@ -21,7 +21,9 @@ Bars:
                            batch, on every replay.
   greedy tokens            each chosen token's fp32-oracle logit within
                            0.15 of that step's maximum (a near-tie may go
-                           either way in bf16; a wrong token cannot).
+                           either way in bf16; a wrong token cannot); the
+                           graph and eager engines token for token up to a
+                           first difference at a near-tie.
 """
 import pytest
 import torch
@@ -534,8 +536,21 @@ def test_engine_greedy_generation_vs_oracle(gpu):
         chosen = steps[torch.arange(len(out)), torch.tensor(out)]
         gap = (steps.max(-1).values - chosen).max().item()
         assert gap <= 0.15, (i, gap)
-    agree = sum(a == b for x, y in zip(results[True], results[False]) for a, b in zip(x, y))
-    assert agree >= 0.9 * sum(new), "graph and eager engines disagree beyond near-ties"
+    # graph and eager engines: token for token up to a first difference, which
+    # may only come at a near-tie (the decode attention splits a padded bucket
+    # differently from the unpadded eager batch; every other kernel of the
+    # step is row-invariant)
+    for i, (p, x, y) in enumerate(zip(prompts, results[True], results[False])):
+        s = next((j for j, (a, b) in enumerate(zip(x, y)) if a != b), None)
+        if s is None:
+            continue
+        ctx = torch.tensor(p + x[:s])
+        ref = om.qwen3_logits_ref(state, cfg, ctx)[-1]
+        ref16 = om.qwen3_logits_ref(state, cfg, ctx, dtype=torch.bfloat16)[-1]
+        bar = 2 * (ref16 - ref).abs().max().item()
+        d = abs(ref[x[s]].item() - ref[y[s]].item())
+        announce(f"  request {i}: graph/eager first differ at step {s}, gap {d:.4f}, bar {bar:.4f}")
+        assert d <= bar, (i, s, d, bar)
 
     # eos: a token the model does produce stops each request right after it,
     # also when it is seen one pipelined step late

@@ -53,14 +53,16 @@ def qwen3_0p6b(gpu):
     return model, state, cfg, prompts
 
 
-def _pool(cfg, gpu, n_req, max_seq):
+def _pool(cfg, gpu, n_req, max_seq, graph_rows=0):
+    """A pool for n_req requests of up to max_seq tokens, plus graph_rows
+    placeholder handles (one page each) and the graph runner's dummy row."""
     from qwen3_engine_from_scratch_amd.PagedKVcache import KVCachePool
 
     bs = 16
-    blocks = n_req * ((max_seq + bs - 1) // bs) + 2 * n_req + 16
+    blocks = n_req * ((max_seq + bs - 1) // bs) + graph_rows + n_req + 16
     return KVCachePool(blocks, cfg.num_hidden_layers, bs, cfg.num_key_value_heads, cfg.head_dim,
                        device=gpu, dtype=torch.bfloat16, max_seq_len=max_seq,
-                       max_requests=2 * n_req + 8)
+                       max_requests=graph_rows + n_req + 8)
 
 
 def _rel(a, b):
@@ -106,7 +108,7 @@ def test_qwen3_0p6b_engine_greedy_vs_oracle(gpu, qwen3_0p6b):
     from qwen3_engine_from_scratch_amd.engine import Engine, GenRequest
 
     model, state, cfg, prompts = qwen3_0p6b
-    pool = _pool(cfg, gpu, N_PROMPTS, CAP + NEW + 8)
+    pool = _pool(cfg, gpu, N_PROMPTS, CAP + NEW + 8, graph_rows=64)
     announce(f"Qwen3-0.6B engine: {N_PROMPTS} requests, prompts <= {CAP}, {NEW} greedy tokens")
     eng = Engine(model, pool, max_batch=64, use_graph=True)
     reqs = [GenRequest(i, p, NEW) for i, p in enumerate(prompts)]
