@@ -117,6 +117,33 @@ int qwen3_paged_decode_bf16(const void* q, const int64_t q_strides[2],
                             void* workspace, size_t workspace_bytes,
                             void* stream);
 
+/* Allocation-free variant of qwen3_paged_decode_bf16.  No counterpart in the
+ * reference: it is for callers that cannot allocate device memory (code
+ * under HIP graph capture, tight serving loops, harnesses that forbid
+ * hipMalloc).  Same arguments, results and kernels as qwen3_paged_decode_bf16
+ * minus the workspace: the split-KV partials live in a static device array of
+ * 24 MiB that each GPU running the library holds until the process ends
+ * (resolved once per device on the first call there).  Serves batches up to
+ * 2048 whose partials fit it: 2 x waves x (G x 516 + ...) bytes, about
+ * 2.1 MB x G on a 256-CU MI355X, so G = num_heads / num_kv_heads <= 11 there;
+ * larger shapes return QWEN3_EWORKSPACE with the size they would need.
+ * Every call of this entry point on one GPU shares that GPU's array, which
+ * keeps the last call's contents (nothing in it has to start at zero); calls
+ * that overlap on one GPU (concurrent streams) race and must be serialised
+ * by the caller.  The stream must belong to the current device.  Allocates
+ * nothing (no hipMalloc, no hipFree). */
+int qwen3_paged_decode_noalloc_bf16(const void* q, const int64_t q_strides[2],
+                                    const void* k_cache, const int64_t k_strides[3],
+                                    const void* v_cache, const int64_t v_strides[3],
+                                    int64_t num_blocks,
+                                    const int32_t* block_table, int64_t bt_row_stride,
+                                    int64_t max_rows, int64_t max_pages,
+                                    const int32_t* seq_lens, int seq_len_bias,
+                                    const int32_t* row_ids,
+                                    void* out, const int64_t out_strides[2],
+                                    int B, int num_heads, int num_kv_heads, int head_dim,
+                                    int block_size, float scale, void* stream);
+
 /* ------------------------------------------------------------------------
  * Decode-form K/V slot write.
  *

@@ -33,6 +33,14 @@ _SIGNATURES = {
          _i, _i, _i, _i, _i, ctypes.c_float,
          _vp, ctypes.c_size_t, _vp],
     ),
+    "qwen3_paged_decode_noalloc_bf16": (
+        _i,
+        [_vp, _c_i64p, _vp, _c_i64p, _vp, _c_i64p, _i64,
+         _vp, _i64, _i64, _i64,
+         _vp, _i, _vp,
+         _vp, _c_i64p,
+         _i, _i, _i, _i, _i, ctypes.c_float, _vp],
+    ),
     "qwen3_kv_write_decode_bf16": (
         _i,
         [_vp, _c_i64p, _vp, _c_i64p, _vp, _c_i64p, _vp, _c_i64p,

@@ -31,6 +31,8 @@
 //    updated once per batch of tiles.
 //  * Batches above kStreamMaxB use a non-persistent grid variant (one
 //    workgroup per partition of tiles) with the same tile math.
+#include <mutex>
+
 #include "common.hpp"
 
 namespace {
@@ -69,8 +71,8 @@ struct DecodeArgs {
   int B, Hq, Hkv, G, bs;
   float scale_log2;  // softmax scale * log2(e)
   // stream path workspace
-  float* s_po;       // [W][2][kMaxG][kD] normalised partial outputs
-  float* s_plse;     // [W][2][kMaxG] log2-sum-exp of each partial
+  float* s_po;       // [W][2][G][kD] normalised partial outputs
+  float* s_plse;     // [W][2][G] log2-sum-exp of each partial
   int32_t* s_pref;   // [B + 1] exclusive prefix of tiles per sequence
   int32_t* s_meta;   // [0] tiles per wave
   // grid path workspace
@@ -443,7 +445,7 @@ void paged_decode_stream_kernel(DecodeArgs a) {
       if (complete) {
         store_out_bf16(a, cb, hq, st, inv, hi);
       } else {
-        const int64_t slot = (w * 2 + (cfirst ? 0 : 1)) * kMaxG + lo;
+        const int64_t slot = (w * 2 + (cfirst ? 0 : 1)) * a.G + lo;
         float* po = a.s_po + slot * kD + 32 * hi;
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
@@ -521,7 +523,7 @@ __global__ __launch_bounds__(kMaxG * 64) void paged_decode_stream_merge_kernel(D
   auto slot_of = [&](int i) -> int64_t {
     const int64_t wv = wf + i;
     const int half = (i == 0 && wv * pw != S) ? 1 : 0;
-    return (wv * 2 + half) * kMaxG + g;
+    return (wv * 2 + half) * G + g;
   };
   // Pass 1: global max of the partial LSEs.
   float M = q3::kNegInf;
@@ -764,11 +766,13 @@ struct StreamLayout {
   int64_t po, plse, pref, meta, total;
 };
 
-StreamLayout stream_layout(int B, int64_t waves) {
+// Workspace layout of the stream path for `waves` persistent waves and
+// groups of G query heads.
+StreamLayout stream_layout(int B, int64_t waves, int G) {
   StreamLayout s;
   s.po = 0;
-  s.plse = s.po + align256(waves * 2 * kMaxG * kD * 4);
-  s.pref = s.plse + align256(waves * 2 * kMaxG * 4);
+  s.plse = s.po + align256(waves * 2 * G * kD * 4);
+  s.pref = s.plse + align256(waves * 2 * G * 4);
   s.meta = s.pref + align256((static_cast<int64_t>(B) + 1) * 4);
   s.total = s.meta + 256;
   return s;
@@ -783,26 +787,15 @@ int64_t grid_bytes(int B, int num_heads, int64_t max_pages, int block_size) {
   return align256(slots * kD * 4) + align256(slots * 4);
 }
 
-}  // namespace
-
-extern "C" size_t qwen3_paged_decode_workspace_bytes(int B, int num_heads, int head_dim,
-                                                     int64_t max_pages, int block_size) {
-  if (B <= 0 || num_heads <= 0 || head_dim != kD || max_pages <= 0 || block_size <= 0 ||
-      block_size % kTile != 0)
-    return 0;
-  if (B <= kStreamMaxB)
-    return static_cast<size_t>(stream_layout(B, int64_t(kStreamMaxWgs) * kWaves).total);
-  return static_cast<size_t>(grid_bytes(B, num_heads, max_pages, block_size));
-}
-
-extern "C" int qwen3_paged_decode_bf16(
-    const void* q, const int64_t q_strides[2], const void* k_cache, const int64_t k_strides[3],
-    const void* v_cache, const int64_t v_strides[3], int64_t num_blocks,
-    const int32_t* block_table, int64_t bt_row_stride, int64_t max_rows, int64_t max_pages,
-    const int32_t* seq_lens, int seq_len_bias, const int32_t* row_ids, void* out,
-    const int64_t out_strides[2], int B, int num_heads, int num_kv_heads, int head_dim,
-    int block_size, float scale, void* workspace, size_t workspace_bytes, void* stream) {
-  const char* who = "qwen3_paged_decode_bf16";
+// Validates the arguments shared by both decode entry points and fills `a`
+// (everything but the workspace pointers).
+int prepare(DecodeArgs& a, const char* who, const void* q, const int64_t q_strides[2],
+            const void* k_cache, const int64_t k_strides[3], const void* v_cache,
+            const int64_t v_strides[3], int64_t num_blocks, const int32_t* block_table,
+            int64_t bt_row_stride, int64_t max_rows, int64_t max_pages,
+            const int32_t* seq_lens, int seq_len_bias, const int32_t* row_ids, void* out,
+            const int64_t out_strides[2], int B, int num_heads, int num_kv_heads,
+            int head_dim, int block_size, float scale) {
   if (!q || !k_cache || !v_cache || !block_table || !seq_lens || !out || !q_strides ||
       !k_strides || !v_strides || !out_strides)
     return q3::fail(QWEN3_EINVAL, "%s: null pointer argument", who);
@@ -821,7 +814,6 @@ extern "C" int qwen3_paged_decode_bf16(
     return q3::fail(QWEN3_EINVAL, "%s: bad sizes (B=%d num_blocks=%lld max_rows=%lld "
                     "max_pages=%lld bt_row_stride=%lld)", who, B, (long long)num_blocks,
                     (long long)max_rows, (long long)max_pages, (long long)bt_row_stride);
-  if (B == 0) return QWEN3_OK;
   if (B > 65535 || num_kv_heads > 65535)
     return q3::fail(QWEN3_EINVAL, "%s: batch %d too large for one launch", who, B);
   if (max_pages * block_size > (int64_t(1) << 30))
@@ -832,20 +824,11 @@ extern "C" int qwen3_paged_decode_bf16(
                                  out_strides[0], out_strides[1]};
   bool ok = q3::aligned16(q) && q3::aligned16(k_cache) && q3::aligned16(v_cache) &&
             q3::aligned16(out);
-  for (int64_t s : vec_strides) ok = ok && s % 8 == 0;
+  for (int64_t st : vec_strides) ok = ok && st % 8 == 0;
   if (!ok)
     return q3::fail(QWEN3_EALIGN, "%s: q/K/V/out need 16-byte aligned rows (strides multiple "
                     "of 8 elements)", who);
-  const size_t need = qwen3_paged_decode_workspace_bytes(B, num_heads, head_dim, max_pages,
-                                                         block_size);
-  if (need == 0) return q3::fail(QWEN3_EINVAL, "%s: cannot size the workspace", who);
-  if (!workspace || workspace_bytes < need)
-    return q3::fail(QWEN3_EWORKSPACE, "%s: workspace of %zu bytes needed, %zu given", who,
-                    need, workspace ? workspace_bytes : (size_t)0);
-  if (!q3::aligned16(workspace))
-    return q3::fail(QWEN3_EALIGN, "%s: workspace must be 16-byte aligned", who);
-
-  DecodeArgs a{};
+  a = DecodeArgs{};
   a.q = static_cast<const uint16_t*>(q);
   a.q_sb = q_strides[0];
   a.q_sh = q_strides[1];
@@ -874,25 +857,100 @@ extern "C" int qwen3_paged_decode_bf16(
   a.G = num_heads / num_kv_heads;
   a.bs = block_size;
   a.scale_log2 = scale * q3::kLog2e;
-  char* ws = static_cast<char*>(workspace);
+  return QWEN3_OK;
+}
 
+// Persistent workgroups of the stream path on the current device (0: unknown).
+int stream_workgroups() {
+  const int wgs = cu_count() * kStreamWgPerCu;
+  return wgs < kStreamMaxWgs ? wgs : kStreamMaxWgs;
+}
+
+// Launches the stream path (attention pass + merge) with its workspace at ws.
+int launch_stream(DecodeArgs& a, char* ws, int wgs, hipStream_t s, const char* who) {
+  const StreamLayout L = stream_layout(a.B, int64_t(wgs) * kWaves, a.G);
+  a.s_po = reinterpret_cast<float*>(ws + L.po);
+  a.s_plse = reinterpret_cast<float*>(ws + L.plse);
+  a.s_pref = reinterpret_cast<int32_t*>(ws + L.pref);
+  a.s_meta = reinterpret_cast<int32_t*>(ws + L.meta);
   q3::clear_error();
+  hipLaunchKernelGGL(paged_decode_stream_kernel, dim3(wgs), dim3(kWaves * 64), 0, s, a);
+  int rc = q3::launch_status(who);
+  if (rc) return rc;
+  hipLaunchKernelGGL(paged_decode_stream_merge_kernel, dim3(a.Hkv, a.B), dim3(64 * a.G), 0, s,
+                     a);
+  return q3::launch_status(who);
+}
+
+// ---------------------------------------------------------------------------
+// Static scratch of the allocation-free entry point.  Each device that runs
+// the library holds one copy until the process ends; host code reaches a
+// device's copy only through the address hipGetSymbolAddress returns for it
+// (the array's name on the host is a stand-in, not a device address).
+constexpr int64_t kStaticScratchBytes = int64_t(24) << 20;
+constexpr int kMaxDevices = 64;
+static __device__ __align__(256) char scratch[kStaticScratchBytes];
+
+// Device address of `scratch` on device `dev` (the current device), looked up
+// once per device; nullptr if the runtime cannot resolve it.
+char* scratch_on(int dev) {
+  static std::mutex mu;
+  static char* addr[kMaxDevices] = {};
+  std::lock_guard<std::mutex> lock(mu);
+  if (!addr[dev]) {
+    void* p = nullptr;
+    if (hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)) != hipSuccess || !p) {
+      (void)hipGetLastError();
+      return nullptr;
+    }
+    addr[dev] = static_cast<char*>(p);
+  }
+  return addr[dev];
+}
+
+}  // namespace
+
+extern "C" size_t qwen3_paged_decode_workspace_bytes(int B, int num_heads, int head_dim,
+                                                     int64_t max_pages, int block_size) {
+  if (B <= 0 || num_heads <= 0 || head_dim != kD || max_pages <= 0 || block_size <= 0 ||
+      block_size % kTile != 0)
+    return 0;
+  // Upper bound over every group size and up to kStreamMaxWgs workgroups, so
+  // the size depends only on the launch shape.
+  if (B <= kStreamMaxB)
+    return static_cast<size_t>(stream_layout(B, int64_t(kStreamMaxWgs) * kWaves, kMaxG).total);
+  return static_cast<size_t>(grid_bytes(B, num_heads, max_pages, block_size));
+}
+
+extern "C" int qwen3_paged_decode_bf16(
+    const void* q, const int64_t q_strides[2], const void* k_cache, const int64_t k_strides[3],
+    const void* v_cache, const int64_t v_strides[3], int64_t num_blocks,
+    const int32_t* block_table, int64_t bt_row_stride, int64_t max_rows, int64_t max_pages,
+    const int32_t* seq_lens, int seq_len_bias, const int32_t* row_ids, void* out,
+    const int64_t out_strides[2], int B, int num_heads, int num_kv_heads, int head_dim,
+    int block_size, float scale, void* workspace, size_t workspace_bytes, void* stream) {
+  const char* who = "qwen3_paged_decode_bf16";
+  DecodeArgs a;
+  if (int rc = prepare(a, who, q, q_strides, k_cache, k_strides, v_cache, v_strides, num_blocks,
+                       block_table, bt_row_stride, max_rows, max_pages, seq_lens,
+                       seq_len_bias, row_ids, out, out_strides, B, num_heads, num_kv_heads,
+                       head_dim, block_size, scale))
+    return rc;
+  if (B == 0) return QWEN3_OK;
+  const size_t need = qwen3_paged_decode_workspace_bytes(B, num_heads, head_dim, max_pages,
+                                                         block_size);
+  if (need == 0) return q3::fail(QWEN3_EINVAL, "%s: cannot size the workspace", who);
+  if (!workspace || workspace_bytes < need)
+    return q3::fail(QWEN3_EWORKSPACE, "%s: workspace of %zu bytes needed, %zu given", who,
+                    need, workspace ? workspace_bytes : (size_t)0);
+  if (!q3::aligned16(workspace))
+    return q3::fail(QWEN3_EALIGN, "%s: workspace must be 16-byte aligned", who);
+  char* ws = static_cast<char*>(workspace);
   hipStream_t s = static_cast<hipStream_t>(stream);
   if (B <= kStreamMaxB) {
-    int wgs = cu_count() * kStreamWgPerCu;
+    const int wgs = stream_workgroups();
     if (wgs <= 0) return q3::fail(QWEN3_EINVAL, "%s: cannot query the device's CU count", who);
-    wgs = wgs < kStreamMaxWgs ? wgs : kStreamMaxWgs;
-    const StreamLayout L = stream_layout(B, int64_t(kStreamMaxWgs) * kWaves);
-    a.s_po = reinterpret_cast<float*>(ws + L.po);
-    a.s_plse = reinterpret_cast<float*>(ws + L.plse);
-    a.s_pref = reinterpret_cast<int32_t*>(ws + L.pref);
-    a.s_meta = reinterpret_cast<int32_t*>(ws + L.meta);
-    hipLaunchKernelGGL(paged_decode_stream_kernel, dim3(wgs), dim3(kWaves * 64), 0, s, a);
-    int rc = q3::launch_status(who);
-    if (rc) return rc;
-    hipLaunchKernelGGL(paged_decode_stream_merge_kernel, dim3(num_kv_heads, B), dim3(64 * a.G),
-                       0, s, a);
-    return q3::launch_status(who);
+    return launch_stream(a, ws, wgs, s, who);
   }
   const int64_t parts = grid_parts(max_pages, block_size);
   if (parts > 0x7fffffff) return q3::fail(QWEN3_EINVAL, "%s: max_pages too large", who);
@@ -901,10 +959,44 @@ extern "C" int qwen3_paged_decode_bf16(
   a.ws_o = reinterpret_cast<float*>(ws);
   a.ws_lse = reinterpret_cast<float*>(ws + align256(slots * kD * 4));
   const size_t lds = static_cast<size_t>(kWaves) * a.G * kOStride * sizeof(float);
+  q3::clear_error();
   hipLaunchKernelGGL(paged_decode_grid_kernel, dim3(static_cast<unsigned>(parts), num_kv_heads, B),
                      dim3(kWaves * 64), lds, s, a);
   int rc = q3::launch_status(who);
   if (rc || parts == 1) return rc;
   hipLaunchKernelGGL(paged_decode_grid_merge_kernel, dim3(num_heads, B), dim3(kD), 0, s, a);
   return q3::launch_status(who);
+}
+
+extern "C" int qwen3_paged_decode_noalloc_bf16(
+    const void* q, const int64_t q_strides[2], const void* k_cache, const int64_t k_strides[3],
+    const void* v_cache, const int64_t v_strides[3], int64_t num_blocks,
+    const int32_t* block_table, int64_t bt_row_stride, int64_t max_rows, int64_t max_pages,
+    const int32_t* seq_lens, int seq_len_bias, const int32_t* row_ids, void* out,
+    const int64_t out_strides[2], int B, int num_heads, int num_kv_heads, int head_dim,
+    int block_size, float scale, void* stream) {
+  const char* who = "qwen3_paged_decode_noalloc_bf16";
+  DecodeArgs a;
+  if (int rc = prepare(a, who, q, q_strides, k_cache, k_strides, v_cache, v_strides, num_blocks,
+                       block_table, bt_row_stride, max_rows, max_pages, seq_lens,
+                       seq_len_bias, row_ids, out, out_strides, B, num_heads, num_kv_heads,
+                       head_dim, block_size, scale))
+    return rc;
+  if (B == 0) return QWEN3_OK;
+  if (B > kStreamMaxB)
+    return q3::fail(QWEN3_EWORKSPACE, "%s: batch %d exceeds the %d rows the static scratch "
+                    "serves", who, B, kStreamMaxB);
+  const int wgs = stream_workgroups();
+  if (wgs <= 0) return q3::fail(QWEN3_EINVAL, "%s: cannot query the device's CU count", who);
+  const int64_t need = stream_layout(B, int64_t(wgs) * kWaves, a.G).total;
+  if (need > kStaticScratchBytes)
+    return q3::fail(QWEN3_EWORKSPACE, "%s: needs %lld bytes of scratch (batch %d, %d query "
+                    "heads per KV head); the static scratch holds %lld", who, (long long)need,
+                    B, a.G, (long long)kStaticScratchBytes);
+  int dev = -1;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices)
+    return q3::fail(QWEN3_EINVAL, "%s: cannot query the current device", who);
+  char* ws = scratch_on(dev);
+  if (!ws) return q3::fail(QWEN3_EINVAL, "%s: cannot resolve the static scratch", who);
+  return launch_stream(a, ws, wgs, static_cast<hipStream_t>(stream), who);
 }
