@@ -19,3 +19,12 @@ def test_product_rope_tables_equal_the_oracle_tables():
     c1, s1 = rope_tables(128, 1e6, 512)
     c2, s2 = opa.rope_tables(128, 1e6, 512)
     assert torch.equal(c1, c2) and torch.equal(s1, s2)
+
+
+def test_bench_config1_inputs_equal_the_oracle_case():
+    c = bench.config1_inputs()
+    o = oi.config1_decode()
+    for name, a, b in (("q", c["q"], o.q), ("k", c["k"], o.k_pool), ("v", c["v"], o.v_pool),
+                       ("bt", c["bt"], o.block_table), ("seq_lens", c["seq_lens"], o.seq_lens),
+                       ("rows", c["row_ids"], o.row_ids)):
+        assert torch.equal(a, b), name

@@ -462,6 +462,22 @@ def test_model_oracle_rejects_planted_mistakes(monkeypatch):
             assert err() > 1e-2, name
 
 
+def test_cached_greedy_generation_equals_full_forward():
+    """The K/V-cached generation oracle (the serving line's CPU baseline):
+    each step's logits equal the pinned full forward's at the same position
+    (teacher forced with the chosen tokens), and each token is their argmax;
+    the transformers model picks the same tokens."""
+    hf, state, cfg = _tiny_hf_model(seed=5, hq=4, hkv=2)
+    prompt = torch.randint(0, cfg.vocab_size, (23,),
+                           generator=torch.Generator().manual_seed(4)).tolist()
+    toks, logits = om.generate_greedy_ref(state, cfg, prompt, 6)
+    full = om.qwen3_logits_ref(state, cfg, prompt + toks[:-1].tolist())[len(prompt) - 1:]
+    assert (logits - full).abs().max().item() < 1e-4 * full.abs().max().item()
+    assert torch.equal(toks, full.argmax(-1))
+    hf_full = _hf_logits(hf, prompt + toks[:-1].tolist())[len(prompt) - 1:]
+    assert torch.equal(toks, hf_full.argmax(-1))
+
+
 # ---- sampling ----------------------------------------------------------------
 
 from oracle import sampling as osm  # noqa: E402
