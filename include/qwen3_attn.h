@@ -226,14 +226,21 @@ int qwen3_kv_write_slots_bf16(const void* k_new, const int64_t k_new_strides[2],
  *   k, v      (total_tokens, num_kv_heads, head_dim), strides *_strides[0..1]
  *   cu_seqlens int32 (num_seqs + 1,) on the device
  *   max_seqlen host-side upper bound of the sequence lengths (sizes the grid;
- *             the reference syncs cu_seqlens to the host to get it, :177-178)
- *   workspace  optional (NULL: static schedule): qwen3_varlen_prefill_
- *             workspace_bytes() bytes of device memory, zeroed before its
- *             first use; every call leaves it zeroed.  With it a batch
- *             large enough for eight-wave workgroups has its work items
- *             dealt from counters as workgroups finish (heaviest first);
- *             smaller batches keep the static order.  Concurrent calls
- *             need separate workspaces.
+ *             the reference syncs cu_seqlens to the host to get it, :177-178).
+ *             Contract: no sequence is longer.  Rows of a longer sequence
+ *             past the first max_seqlen rounded up to the kernel's query
+ *             tile are not written; a larger bound only costs empty work
+ *             items and gives the same bits.
+ *   workspace  optional (NULL: static schedule, no split items):
+ *             qwen3_varlen_prefill_workspace_bytes() bytes (about 35 MB) of
+ *             device memory, zeroed before its first use; every call leaves
+ *             its counters at zero.  With it a batch large enough for
+ *             eight-wave workgroups has its work items dealt from counters
+ *             as workgroups finish (heaviest first), and a causal batch with
+ *             fewer work items than resident workgroups has its heaviest
+ *             items cut into two key ranges whose partial states (the last
+ *             35 MB) meet in the workspace -- the same bits whichever half
+ *             finishes first.  Concurrent calls need separate workspaces.
  * Supported: head_dim 128, num_heads / num_kv_heads in [1, 16].
  * ---------------------------------------------------------------------- */
 size_t qwen3_varlen_prefill_workspace_bytes(void);

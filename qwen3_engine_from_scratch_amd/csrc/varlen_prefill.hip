@@ -51,6 +51,8 @@ constexpr int kMaxSeqs = 256;             // persistent path: sequences ranked i
 constexpr int kScanMax = 1024;            // persistent path: query-tile ranks in LDS
 constexpr int kPools = 8;                 // dynamic schedule: one item pool per XCD
 constexpr int kPoolStride = 32;           // counters 128 bytes apart
+constexpr int kMaxSplits = 256;           // work items cut in two per call, at most
+constexpr int kSplitSlotFloats = 8 * 64 * 66;  // eight waves x 64 lanes x (64 sums, max, sum)
 static_assert(dma_per_wave<4>() == kMaxDma && dma_per_wave<8>() == 2, "tile / workgroup shape");
 
 typedef __attribute__((address_space(3))) void lds_void_t;
@@ -76,6 +78,10 @@ struct PrefillArgs {
   float scale_log2;
   int causal;
   uint32_t* ctr;  // nullable: [32 p] next item of pool p, [32 kPools] workgroups done (zero between calls)
+  // Split work items (split kernel only): per slot a ticket and a ready
+  // flag (zero between calls) and the first finisher's partial state.
+  uint32_t* split_ctr;  // [kMaxSplits][2]
+  float* split_buf;     // [kMaxSplits][kSplitSlotFloats]
 };
 
 // The staged tiles of one workgroup: two K and two V buffers.
@@ -230,11 +236,88 @@ __device__ __forceinline__ void wait_loads() {
   __builtin_amdgcn_s_waitcnt(0x0f70);
 }
 
-// One work item: query tile mt of sequence seq for head group hg.  Every
-// thread of the workgroup calls it.
-template <int W>
+// Partial state of one wave of a split item, in its slot: accumulators as
+// 16 float4 rows of 64 lanes, then (max, sum share) per lane.  Written and
+// read with device-scope accesses (sc1: written through to, and read from,
+// the point where all XCDs' L2s agree), so the hand-off needs no L2
+// write-back or invalidation, which would stall the whole XCD.
+constexpr int kCpolDevice = 16;  // sc1
+constexpr int kSlotMlOffset = 8 * 64 * 64 * 4;  // bytes before the (max, sum) pairs
+
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t slot_rsrc(float* slot) {
+  return __builtin_amdgcn_make_buffer_rsrc(slot, 0, kSplitSlotFloats * 4, 0x00020000);
+}
+
+__device__ __forceinline__ void save_partial(__amdgpu_buffer_rsrc_t slot, int wave, int lane,
+                                             float m_run, float l_run, const q3::f32x16 (&acc)[4]) {
+#pragma unroll
+  for (int db = 0; db < 4; ++db)
+#pragma unroll
+    for (int r4 = 0; r4 < 4; ++r4) {
+      const q3::f32x4 v = {acc[db][4 * r4], acc[db][4 * r4 + 1], acc[db][4 * r4 + 2],
+                           acc[db][4 * r4 + 3]};
+      __builtin_amdgcn_raw_buffer_store_b128(
+          __builtin_bit_cast(q3::u32x4, v), slot,
+          static_cast<uint32_t>(((wave * 16 + db * 4 + r4) * 64 + lane) * 16), 0, kCpolDevice);
+    }
+  const uint32_t ml = kSlotMlOffset + (wave * 64 + lane) * 8;
+  __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(m_run), slot, ml, 0, kCpolDevice);
+  __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(l_run), slot, ml + 4, 0, kCpolDevice);
+}
+
+// Folds the other part's saved state into st (both relative to their own
+// running max; the result is relative to the larger one).  The sums are
+// formed as part 0 * its weight + part 1 * its weight whichever part merges,
+// so the output does not depend on which part finished first.
+__device__ __forceinline__ void merge_partial(__amdgpu_buffer_rsrc_t slot, int wave, int lane,
+                                              bool own_first, float& m_run, float& l_run,
+                                              q3::f32x16 (&acc)[4]) {
+  // Every load in flight at once: one memory round trip.
+  const uint32_t ml = kSlotMlOffset + (wave * 64 + lane) * 8;
+  const float om = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(slot, ml, 0, kCpolDevice));
+  const float ol =
+      __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(slot, ml + 4, 0, kCpolDevice));
+  q3::f32x4 v[16];
+#pragma unroll
+  for (int i = 0; i < 16; ++i)
+    v[i] = __builtin_bit_cast(
+        q3::f32x4, __builtin_amdgcn_raw_buffer_load_b128(
+                       slot, static_cast<uint32_t>(((wave * 16 + i) * 64 + lane) * 16), 0,
+                       kCpolDevice));
+  __builtin_amdgcn_sched_barrier(0);
+  const float m = fmaxf(m_run, om);
+  if (m == q3::kNegInf) return;  // no key reached this row in either part
+  const float a_own = q3::fast_exp2(m_run - m);  // exp2(-inf) = 0
+  const float a_oth = q3::fast_exp2(om - m);
+  const float w0 = own_first ? a_own : a_oth, w1 = own_first ? a_oth : a_own;
+  m_run = m;
+  {
+    const float x0 = own_first ? l_run : ol, x1 = own_first ? ol : l_run;
+    l_run = __builtin_fmaf(x1, w1, x0 * w0);
+  }
+#pragma unroll
+  for (int i = 0; i < 16; ++i)
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const float own = acc[i >> 2][4 * (i & 3) + e];
+      const float x0 = own_first ? own : v[i][e], x1 = own_first ? v[i][e] : own;
+      acc[i >> 2][4 * (i & 3) + e] = __builtin_fmaf(x1, w1, x0 * w0);
+    }
+}
+
+// One work item: query tile mt of sequence seq for head group hg, over all
+// of its key tiles (part < 0) or, in the split kernel, over the first
+// (part 0) or second (part 1) half of them.  The two parts of a split item
+// meet through split slot `slot`: the first to finish saves its partial
+// state and raises the slot's ready flag; the second waits for that flag
+// (the first is past all its work by then, so the wait is short), merges
+// and writes the output, then leaves the slot's ticket and flag at zero.
+// Every thread of the workgroup calls it.
+template <int W, bool Split = false>
 __device__ __forceinline__ void prefill_item(const PrefillArgs& a, const LaneOffsets& off,
-                                             int seq, int hg, int mt, const TileBufs& tb) {
+                                             int seq, int hg, int mt, const TileBufs& tb,
+                                             int part = -1, int slot = 0,
+                                             uint32_t* s_role = nullptr) {
   const int64_t start = a.cu[seq];
   const int64_t end = a.cu[seq + 1];
   if (start < 0 || end > a.total || end <= start) return;
@@ -255,8 +338,10 @@ __device__ __forceinline__ void prefill_item(const PrefillArgs& a, const LaneOff
 
   const int kend = a.causal ? min(len, m0 + a.rows) : len;
   const int n_tiles = (kend + kBN - 1) / kBN;
+  const int t0 = Split && part == 1 ? n_tiles / 2 : 0;
+  const int t1 = Split && part == 0 ? n_tiles / 2 : n_tiles;
 
-  tile_dma<W>(a, off, start, len, kvh, 0, tb.k0, tb.v0, wave);
+  tile_dma<W>(a, off, start, len, kvh, t0 * kBN, tb.k0, tb.v0, wave);
 
   // Q^T as the B operand: lane (query l32, k-group hl), chunk c: dims
   // c*16 + 8*hl .. +7.
@@ -287,7 +372,7 @@ __device__ __forceinline__ void prefill_item(const PrefillArgs& a, const LaneOff
 
   auto tile = [&](int it, const uint16_t* kt, const uint16_t* vt, uint16_t* nk, uint16_t* nv) {
     const int n0 = it * kBN;
-    if (it + 1 < n_tiles) tile_dma<W>(a, off, start, len, kvh, n0 + kBN, nk, nv, wave);
+    if (it + 1 < t1) tile_dma<W>(a, off, start, len, kvh, n0 + kBN, nk, nv, wave);
 
     // Causal: the tile is entirely above this wave's last query row.
     const bool wave_skip = !wave_active || (a.causal && n0 > wave_last_q);
@@ -391,9 +476,43 @@ __device__ __forceinline__ void prefill_item(const PrefillArgs& a, const LaneOff
     __syncthreads();
   };
 
-  for (int it = 0; it < n_tiles; it += 2) {
+  for (int it = t0; it < t1; it += 2) {
     tile(it, tb.k0, tb.v0, tb.k1, tb.v1);
-    if (it + 1 < n_tiles) tile(it + 1, tb.k1, tb.v1, tb.k0, tb.v0);
+    if (it + 1 < t1) tile(it + 1, tb.k1, tb.v1, tb.k0, tb.v0);
+  }
+
+  if constexpr (Split) {
+    if (part >= 0) {
+      uint32_t* ticket = a.split_ctr + 2 * slot;
+      uint32_t* ready = ticket + 1;
+      const __amdgpu_buffer_rsrc_t saved =
+          slot_rsrc(a.split_buf + static_cast<int64_t>(slot) * kSplitSlotFloats);
+      if (tid == 0)
+        *s_role = __hip_atomic_fetch_add(ticket, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      __syncthreads();
+      if (*s_role == 0) {
+        save_partial(saved, wave, lane, m_run, l_run, acc);
+        wait_loads();  // this wave's device-scope saves are complete
+        __syncthreads();
+        if (tid == 0) __hip_atomic_store(ready, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        return;
+      }
+      if (tid == 0) {
+        // Bounded: with the ticket taken, the other part only has its
+        // saves left.  (A workspace not zeroed before its first call could
+        // leave the flag down; the cap ends the wait all the same.)
+        for (int spin = 0; spin < (1 << 22); ++spin) {
+          if (__hip_atomic_load(ready, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) != 0u) break;
+          __builtin_amdgcn_s_sleep(1);
+        }
+      }
+      __syncthreads();  // the saves are read (device scope) only after the flag
+      merge_partial(saved, wave, lane, part == 0, m_run, l_run, acc);
+      if (tid == 0) {
+        __hip_atomic_store(ticket, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        __hip_atomic_store(ready, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      }
+    }
   }
 
   l_run = cross_half_sum(l_run);
@@ -475,43 +594,19 @@ __device__ __forceinline__ int block_exclusive_scan(int* v, int n, int* s_wsum) 
   return total;
 }
 
-// Persistent grid (CUs x resident workgroups).  Every workgroup builds the
-// same compact list of non-empty items ordered heaviest first (query tiles
-// of the highest index first; within one, longest sequences first, head
-// group fastest), and item i goes to XCD i % 8, so one head group's K/V
-// tiles stay in one XCD's L2.  Workgroup w takes item w first (the
-// heaviest items, one per workgroup).  With counters in the workspace (and
-// a multiple of 8 head groups) each XCD's workgroups then take that XCD's
-// remaining items from its pool as they finish -- longest-processing-time-
-// first list scheduling: a workgroup busy with a heavy item takes no more
-// until the others have theirs -- asking for the next one while the current
-// one runs, and take what other pools have left once theirs is empty.
-// Without them they take their share in a snake order over rounds
-// (mirroring whole groups of 8 positions so item i stays on XCD i % 8).
-#ifndef Q3_PREFILL_PERSISTENT_WAVES_PER_EU
-#define Q3_PREFILL_PERSISTENT_WAVES_PER_EU 2
-#endif
+// Builds, in every workgroup's LDS, the compact list of the non-empty items
+// (query tile, sequence, head group) ordered heaviest first: query tiles of
+// the highest index first; within one, longest sequences first (ties by
+// index), head group fastest.  s_first[r] = items before query-tile rank r
+// (r = n_mtiles - 1 - mt); s_len[t] = sequence t's length (0 for a range
+// outside the batch).  Returns the number of items.  Called by all threads
+// of the workgroup.
 template <int W>
-__global__ __launch_bounds__(W * 64)
-__attribute__((amdgpu_waves_per_eu(Q3_PREFILL_PERSISTENT_WAVES_PER_EU, Q3_PREFILL_PERSISTENT_WAVES_PER_EU)))
-void varlen_prefill_persistent_kernel(PrefillArgs a) {
-  Q3_PREFILL_TILE_BUFFERS;
-  __shared__ int s_len[kMaxSeqs];
-  __shared__ int s_sorted[kMaxSeqs];
-  __shared__ int s_first[kScanMax];  // items before m-tile rank r (r = n_mtiles-1-mt)
-  __shared__ int s_wsum[W];
+__device__ __forceinline__ int build_items(const PrefillArgs& a, int* s_len, int* s_sorted,
+                                           int* s_first, int* s_wsum) {
   const int tid = threadIdx.x;
   const int S = a.num_seqs;
   const int nm = a.n_mtiles;
-  // Workgroup 0 clears the counters before its first barrier (a workspace
-  // never used, or left mid-call, still gives every item to some workgroup:
-  // workgroup 0 takes items, from every pool, until all are done, and an
-  // item taken twice is computed twice with the same result).
-  if (a.ctr && blockIdx.x == 0 && tid <= kPools) {
-    const uint32_t prev = atomicExch(a.ctr + tid * kPoolStride, 0u);
-    asm volatile("" ::"v"(prev));  // performed before this thread reaches the barriers below
-  }
-
   for (int t = tid; t < S; t += W * 64) {
     const int64_t s0 = a.cu[t], s1 = a.cu[t + 1];
     const bool ok = s0 >= 0 && s1 <= a.total && s1 > s0;
@@ -541,21 +636,67 @@ void varlen_prefill_persistent_kernel(PrefillArgs a) {
     s_first[r] = lo * a.groups;
   }
   __syncthreads();
-  const int T = block_exclusive_scan<W>(s_first, nm, s_wsum);
+  return block_exclusive_scan<W>(s_first, nm, s_wsum);
+}
 
-  // Item i (uniform, read from LDS): made scalar with readfirstlane so the
-  // item's indices and bounds live in SGPRs.
+// Coordinates of item i of that list (uniform, read from LDS): made scalar
+// with readfirstlane so the item's indices and bounds live in SGPRs.
+__device__ __forceinline__ void item_at(const PrefillArgs& a, int64_t i64, const int* s_first,
+                                        const int* s_sorted, int& seq, int& hg, int& mt) {
+  const int nm = a.n_mtiles;
+  const int i = __builtin_amdgcn_readfirstlane(static_cast<int>(i64));
+  int lo = 0, hi = nm - 1;  // largest rank r with s_first[r] <= i
+  while (lo < hi) {
+    const int mid = (lo + hi + 1) >> 1;
+    if (__builtin_amdgcn_readfirstlane(s_first[mid]) <= i) lo = mid; else hi = mid - 1;
+  }
+  const int j = i - __builtin_amdgcn_readfirstlane(s_first[lo]);
+  seq = __builtin_amdgcn_readfirstlane(s_sorted[j / a.groups]);
+  hg = j % a.groups;
+  mt = nm - 1 - lo;
+}
+
+// Persistent grid (CUs x resident workgroups).  Every workgroup builds the
+// same compact list of non-empty items ordered heaviest first (query tiles
+// of the highest index first; within one, longest sequences first, head
+// group fastest), and item i goes to XCD i % 8, so one head group's K/V
+// tiles stay in one XCD's L2.  Workgroup w takes item w first (the
+// heaviest items, one per workgroup).  With counters in the workspace (and
+// a multiple of 8 head groups) each XCD's workgroups then take that XCD's
+// remaining items from its pool as they finish -- longest-processing-time-
+// first list scheduling: a workgroup busy with a heavy item takes no more
+// until the others have theirs -- asking for the next one while the current
+// one runs, and take what other pools have left once theirs is empty.
+// Without them they take their share in a snake order over rounds
+// (mirroring whole groups of 8 positions so item i stays on XCD i % 8).
+#ifndef Q3_PREFILL_PERSISTENT_WAVES_PER_EU
+#define Q3_PREFILL_PERSISTENT_WAVES_PER_EU 2
+#endif
+template <int W>
+__global__ __launch_bounds__(W * 64)
+__attribute__((amdgpu_waves_per_eu(Q3_PREFILL_PERSISTENT_WAVES_PER_EU, Q3_PREFILL_PERSISTENT_WAVES_PER_EU)))
+void varlen_prefill_persistent_kernel(PrefillArgs a) {
+  Q3_PREFILL_TILE_BUFFERS;
+  __shared__ int s_len[kMaxSeqs];
+  __shared__ int s_sorted[kMaxSeqs];
+  __shared__ int s_first[kScanMax];  // items before m-tile rank r (r = n_mtiles-1-mt)
+  __shared__ int s_wsum[W];
+  const int tid = threadIdx.x;
+  // Workgroup 0 clears the counters before its first barrier (a workspace
+  // never used, or left mid-call, still gives every item to some workgroup:
+  // workgroup 0 takes items, from every pool, until all are done, and an
+  // item taken twice is computed twice with the same result).
+  if (a.ctr && blockIdx.x == 0 && tid <= kPools) {
+    const uint32_t prev = atomicExch(a.ctr + tid * kPoolStride, 0u);
+    asm volatile("" ::"v"(prev));  // performed before this thread reaches the barriers below
+  }
+
+  const int T = build_items<W>(a, s_len, s_sorted, s_first, s_wsum);
+
   auto run = [&](int64_t i64) {
-    const int i = __builtin_amdgcn_readfirstlane(static_cast<int>(i64));
-    int lo = 0, hi = nm - 1;  // largest rank r with s_first[r] <= i
-    while (lo < hi) {
-      const int mid = (lo + hi + 1) >> 1;
-      if (__builtin_amdgcn_readfirstlane(s_first[mid]) <= i) lo = mid; else hi = mid - 1;
-    }
-    const int j = i - __builtin_amdgcn_readfirstlane(s_first[lo]);
-    const int seq = __builtin_amdgcn_readfirstlane(s_sorted[j / a.groups]);
-    const int hg = j % a.groups;
-    prefill_item<W>(a, off, seq, hg, nm - 1 - lo, tb);
+    int seq, hg, mt;
+    item_at(a, i64, s_first, s_sorted, seq, hg, mt);
+    prefill_item<W>(a, off, seq, hg, mt, tb);
   };
   // One loop and one inlined item body for both orders (each extra call
   // site of `run` costs registers in the tile loop).
@@ -632,6 +773,145 @@ void varlen_prefill_persistent_kernel(PrefillArgs a) {
 // Sizes the items for W waves and launches the persistent grid (CUs x
 // resident workgroups, from the occupancy API) or, past its LDS tables, the
 // flat grid.
+// Split plan of a causal batch (with split slots in the workspace).  An
+// item's work is its key tiles, about (mt + 1) rows / 64 for query tile mt,
+// so the heaviest items are those of the highest query tiles -- the first
+// ranks of the list.  The items of query tiles mt >= ms are cut in two at
+// their middle key tile, ms being the lowest query tile whose items are
+// heavier than the batch's mean work per workgroup (and have at least four
+// key tiles, and fit the slots); a split item's slot is its list index.
+// Entries are then ordered by work in half-tile classes: class k holds the
+// whole items of query tile k / 2 - 1 (k even, below ms) followed by the
+// two parts of each item of query tile k - 1 (at or above ms), classes
+// heaviest first.  s_cls[j] = entries before class 2 n_mtiles - j.
+struct SplitPlan {
+  int ms;  // first split query tile (n_mtiles: none)
+  int E;   // work entries
+  int T;   // items
+};
+
+template <int W>
+__device__ __forceinline__ SplitPlan plan_splits(const PrefillArgs& a, const int* s_len,
+                                                 const int* s_first, int T, int nwg, int* s_cls,
+                                                 int* s_wsum, unsigned long long* s_work) {
+  const int nm = a.n_mtiles;
+  const int tid = threadIdx.x;
+  SplitPlan p{nm, T, T};
+  if (!a.split_buf || !a.causal || 2 * nm > kScanMax) return p;
+  // Key tiles of all items, per head group.
+  if (tid == 0) *s_work = 0ull;
+  __syncthreads();
+  unsigned long long mine = 0;
+  for (int t = tid; t < a.num_seqs; t += W * 64) {
+    const int len = s_len[t];
+    for (int m0 = 0; m0 < len; m0 += a.rows) mine += (min(len, m0 + a.rows) + kBN - 1) / kBN;
+  }
+  if (mine) atomicAdd(s_work, mine);
+  __syncthreads();
+  const unsigned long long work = *s_work * a.groups;
+  const unsigned long long mean = (work + nwg - 1) / nwg;  // key tiles per workgroup
+  // Lowest mt with (mt + 1) rows > mean * 64 and at least four key tiles.
+  int ms = static_cast<int>(min<unsigned long long>(mean * kBN / a.rows, nm));
+  ms = max(ms, 4 * kBN / a.rows - 1);
+  auto before = [&](int r) { return r < nm ? s_first[r] : T; };  // items before rank r
+  while (ms < nm && before(nm - ms) > kMaxSplits) ++ms;
+  if (ms >= nm) return p;
+  p.ms = ms;
+  const int K = 2 * nm;
+  for (int j = tid; j < K; j += W * 64) {
+    const int k = K - j;
+    int cnt = 0;
+    const int mu = k / 2 - 1;  // whole items of query tile mu
+    if ((k & 1) == 0 && mu < ms) cnt += before(nm - mu) - before(nm - 1 - mu);
+    const int mp = k - 1;      // parts of the items of query tile mp
+    if (mp >= ms && mp < nm) cnt += 2 * (before(nm - mp) - before(nm - 1 - mp));
+    s_cls[j] = cnt;
+  }
+  __syncthreads();
+  p.E = block_exclusive_scan<W>(s_cls, K, s_wsum);
+  return p;
+}
+
+// Coordinates of work entry e (uniform): the item (seq, hg, mt), its part
+// (-1: whole) and split slot.
+__device__ __forceinline__ void entry_at(const PrefillArgs& a, const SplitPlan& p, int64_t e64,
+                                         const int* s_first, const int* s_sorted, const int* s_cls,
+                                         int& seq, int& hg, int& mt, int& part, int& slot) {
+  const int nm = a.n_mtiles;
+  part = -1;
+  slot = 0;
+  if (p.ms >= nm) {
+    item_at(a, e64, s_first, s_sorted, seq, hg, mt);
+    return;
+  }
+  const int e = __builtin_amdgcn_readfirstlane(static_cast<int>(e64));
+  const int K = 2 * nm;
+  int lo = 0, hi = K - 1;  // largest class index j with s_cls[j] <= e
+  while (lo < hi) {
+    const int mid = (lo + hi + 1) >> 1;
+    if (__builtin_amdgcn_readfirstlane(s_cls[mid]) <= e) lo = mid; else hi = mid - 1;
+  }
+  const int k = K - lo;
+  int o = e - __builtin_amdgcn_readfirstlane(s_cls[lo]);
+  auto before = [&](int r) {  // items before rank r
+    return r < nm ? __builtin_amdgcn_readfirstlane(s_first[r]) : p.T;
+  };
+  int r;
+  const int mu = k / 2 - 1;
+  bool whole = false;
+  if ((k & 1) == 0 && mu < p.ms) {
+    r = nm - 1 - mu;
+    const int n_whole = before(r + 1) - before(r);
+    whole = o < n_whole;
+    if (!whole) o -= n_whole;
+  }
+  int j;
+  if (whole) {
+    mt = mu;
+    j = o;
+  } else {
+    mt = k - 1;
+    r = nm - 1 - mt;
+    j = o >> 1;
+    part = o & 1;
+    slot = before(r) + j;
+  }
+  seq = __builtin_amdgcn_readfirstlane(s_sorted[j / a.groups]);
+  hg = j % a.groups;
+}
+
+// Small causal batches (fewer items than resident workgroups, so most CUs
+// would otherwise idle while the longest items finish): the same item list,
+// with the heaviest items cut in two (split plan above) and handed out in
+// the snake order of the persistent grid.  A part waits only for a part
+// that has finished its key tiles, so every wait ends.
+template <int W>
+__global__ __launch_bounds__(W * 64) __attribute__((amdgpu_waves_per_eu(2, 2)))
+void varlen_prefill_split_kernel(PrefillArgs a) {
+  Q3_PREFILL_TILE_BUFFERS;
+  __shared__ int s_len[kMaxSeqs];
+  __shared__ int s_sorted[kMaxSeqs];
+  __shared__ int s_first[kScanMax];  // items before m-tile rank r (r = n_mtiles-1-mt)
+  __shared__ int s_cls[kScanMax];    // entries before work class 2 n_mtiles - j
+  __shared__ int s_wsum[W];
+  __shared__ unsigned long long s_work;
+  __shared__ uint32_t s_role;
+  const int T_items = build_items<W>(a, s_len, s_sorted, s_first, s_wsum);
+  const SplitPlan plan =
+      plan_splits<W>(a, s_len, s_first, T_items, gridDim.x, s_cls, s_wsum, &s_work);
+  const int64_t nwg = gridDim.x;
+  const int w = blockIdx.x;
+  const int w_mirror = (gridDim.x / 8 - 1 - w / 8) * 8 + w % 8;
+  int64_t i = w;
+  for (int round = 1; i < plan.E; ++round) {
+    int seq, hg, mt, part, slot;
+    entry_at(a, plan, i, s_first, s_sorted, s_cls, seq, hg, mt, part, slot);
+    prefill_item<W, true>(a, off, seq, hg, mt, tb, part, slot, &s_role);
+    i = static_cast<int64_t>(round) * nwg + ((round & 1) ? w_mirror : w);
+    __syncthreads();  // the entry's LDS tiles are no longer read
+  }
+}
+
 template <int W>
 int launch_prefill(PrefillArgs a, int num_seqs, int max_seqlen, int dev, int cus,
                    hipStream_t s, const char* who) {
@@ -653,7 +933,15 @@ int launch_prefill(PrefillArgs a, int num_seqs, int max_seqlen, int dev, int cus
     occupancy[dev] = per_cu;
   const bool persistent =
       num_seqs <= kMaxSeqs && a.n_mtiles <= kScanMax && cus > 0 && per_cu > 0;
-  if (persistent) {
+  // At most this many items: groups x (query tiles of all rows + one
+  // ragged tile per sequence).
+  const int64_t items_max = static_cast<int64_t>(a.groups) *
+                            (q3::cdiv(a.total, a.rows) + static_cast<int64_t>(num_seqs));
+  if (persistent && a.split_buf && a.causal && 2 * a.n_mtiles <= kScanMax &&
+      items_max < static_cast<int64_t>(cus) * per_cu) {
+    const int wgs = ((cus * per_cu + 7) / 8) * 8;
+    hipLaunchKernelGGL(varlen_prefill_split_kernel<W>, dim3(wgs), dim3(W * 64), 0, s, a);
+  } else if (persistent) {
     const int wgs = ((cus * per_cu + 7) / 8) * 8;  // multiple of 8 for the XCD-preserving snake
     hipLaunchKernelGGL(varlen_prefill_persistent_kernel<W>, dim3(wgs), dim3(W * 64), 0, s, a);
   } else {
@@ -663,11 +951,16 @@ int launch_prefill(PrefillArgs a, int num_seqs, int max_seqlen, int dev, int cus
   return q3::launch_status(who);
 }
 
+// Workspace: schedule counters, split tickets / flags, then split partials.
+constexpr size_t kCtrBytes = (kPools + 1) * kPoolStride * sizeof(uint32_t);
+constexpr size_t kSplitCtrBytes = kMaxSplits * 2 * sizeof(uint32_t);
+constexpr size_t kSplitBufOffset = (kCtrBytes + kSplitCtrBytes + 255) / 256 * 256;
+constexpr size_t kWorkspaceBytes =
+    kSplitBufOffset + static_cast<size_t>(kMaxSplits) * kSplitSlotFloats * sizeof(float);
+
 }  // namespace
 
-extern "C" size_t qwen3_varlen_prefill_workspace_bytes(void) {
-  return (kPools + 1) * kPoolStride * sizeof(uint32_t);
-}
+extern "C" size_t qwen3_varlen_prefill_workspace_bytes(void) { return kWorkspaceBytes; }
 
 extern "C" int qwen3_varlen_prefill_bf16(const void* q, const int64_t q_strides[2],
                                          const void* k, const int64_t k_strides[2],
@@ -751,6 +1044,11 @@ extern "C" int qwen3_varlen_prefill_bf16(const void* q, const int64_t q_strides[
   // of 128..1024 tokens: 229 -> 224 us), while the few rounds of a small
   // batch are paired better by the static snake.
   if (workspace && wide) a.ctr = static_cast<uint32_t*>(workspace);
+  if (workspace) {
+    char* ws = static_cast<char*>(workspace);
+    a.split_ctr = reinterpret_cast<uint32_t*>(ws + kCtrBytes);
+    a.split_buf = reinterpret_cast<float*>(ws + kSplitBufOffset);
+  }
   return wide ? launch_prefill<8>(a, num_seqs, max_seqlen, dev, cus, s, who)
               : launch_prefill<4>(a, num_seqs, max_seqlen, dev, cus, s, who);
 }

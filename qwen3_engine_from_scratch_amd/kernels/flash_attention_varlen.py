@@ -17,8 +17,8 @@ _WORKSPACES: dict = {}
 
 
 def _schedule_workspace(device, lib) -> torch.Tensor:
-    """The per-device zeroed counter buffer of the dynamic item schedule
-    (each call leaves it zeroed)."""
+    """The per-device workspace of the dynamic item schedule and the split
+    items, zeroed once (each call leaves its counters at zero)."""
     ws = _WORKSPACES.get(device)
     if ws is None:
         ws = torch.zeros(int(lib.qwen3_varlen_prefill_workspace_bytes()), dtype=torch.uint8,
@@ -40,10 +40,12 @@ def flash_attention_prefill(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
     head_dim); cu_seqlens: int32 (num_seqs + 1,) cumulative lengths.
     Returns (total_tokens, num_heads, head_dim).  `max_seqlen` (host int) avoids
     the reference's device->host read of cu_seqlens (:177-178); when omitted
-    it is computed the same way the reference does.  `workspace`: the
-    item counter of the dynamic schedule (default: one zeroed buffer per
-    device, kept by this module; concurrent calls on several streams pass
-    their own, zeroed once).
+    it is computed the same way the reference does.  A given max_seqlen must
+    bound every sequence: rows of a longer one past max_seqlen (rounded up to
+    a query tile) are left unwritten.  `workspace`: the dynamic schedule's
+    counters and the split items' partial states (default: one zeroed buffer
+    per device, kept by this module; concurrent calls on several streams
+    pass their own, zeroed once).
     """
     assert q.dim() == 3 and q.shape[1] == num_heads and q.shape[2] == head_dim
     assert k.shape == (q.shape[0], num_kv_heads, head_dim) and v.shape == k.shape

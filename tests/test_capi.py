@@ -96,7 +96,9 @@ def test_prefill_rejects_bad_arguments():
                                              FAKE, 2, 100, 150, H, Hk, D, 0.088, 1, ws, wsb, None)
 
     need = lib.qwen3_varlen_prefill_workspace_bytes()
-    assert need == 9 * 128
+    # 9 schedule counters 128 B apart, 256 split slots' (ticket, flag), then
+    # 256-aligned, 256 slots of 8 waves x 64 lanes x 66 floats
+    assert need == 3328 + 256 * 8 * 64 * 66 * 4
     assert call(ws=FAKE, wsb=need - 1) == -4  # a schedule workspace too small
     assert call(D=256) == -3
     assert call(H=12, Hk=8) == -3

@@ -169,6 +169,69 @@ def test_prefill_counter_schedule_matches_static(gpu):
     assert torch.equal(call(ws), static)
 
 
+SPLIT_CTR = slice(1152, 3200)  # split tickets / ready flags inside the workspace
+SPLIT_BUF = 3328                # first byte of the split partials
+
+
+@pytest.mark.parametrize("lens,hq,hkv", [
+    ([2048], 16, 8),
+    ([1500, 700], 16, 8),
+    ([1200], 32, 8),   # G = 4: 32-row items
+    ([2500], 8, 8),    # G = 1: 128-row items
+])
+def test_prefill_split_items_vs_fp32(gpu, lens, hq, hkv):
+    """Causal batches with fewer work items than resident workgroups take the
+    split kernel: the heaviest items are cut into two key ranges whose
+    partial softmax states meet in the workspace.  The output matches the
+    fp32 closed form, repeated calls give the same bits whichever part
+    finishes first, and every call leaves the split tickets and flags at
+    zero."""
+    from qwen3_engine_from_scratch_amd import _lib
+
+    c = oi.make_prefill_case(lens, hq, hkv, 128, seed=sum(lens) % 97)
+    q, k, v = c.q.to(gpu), c.k.to(gpu), c.v.to(gpu)
+    cu = c.cu_seqlens.to(gpu)
+    lib = _lib.load()
+    ws = torch.zeros(int(lib.qwen3_varlen_prefill_workspace_bytes()), dtype=torch.uint8,
+                     device=gpu)
+
+    def call():
+        out = torch.empty_like(q)
+        rc = lib.qwen3_varlen_prefill_bf16(
+            q.data_ptr(), _lib.strides(q, (0, 1)), k.data_ptr(), _lib.strides(k, (0, 1)),
+            v.data_ptr(), _lib.strides(v, (0, 1)), out.data_ptr(), _lib.strides(out, (0, 1)),
+            cu.data_ptr(), len(lens), max(lens), q.shape[0], hq, hkv, 128, c.scale, 1,
+            ws.data_ptr(), ws.numel(), _lib.stream_of(gpu))
+        _lib.check(rc, "qwen3_varlen_prefill_bf16")
+        torch.cuda.synchronize()
+        return out
+
+    announce(f"prefill split items lens={lens} hq={hq} hkv={hkv}")
+    first = call()
+    assert ws[SPLIT_BUF:].any(), "no item was split"
+    assert not ws[SPLIT_CTR].any(), "split tickets / flags not left at zero"
+    assert_close_attn(first.cpu(), _gpu_ref_fp32(c, gpu, hq // hkv), f"split lens={lens}")
+    for _ in range(3):
+        assert torch.equal(call(), first), "split output depends on the arrival order"
+        assert not ws[SPLIT_CTR].any()
+
+
+def test_prefill_max_seqlen_is_an_upper_bound(gpu):
+    """max_seqlen is a host-side bound (the contract in the header): the
+    exact longest length, the wrapper's own derivation (None) and a larger
+    bound give the same bits."""
+    from qwen3_engine_from_scratch_amd.kernels.flash_attention_varlen import flash_attention_prefill
+
+    lens = [300, 77, 1024, 5]
+    c = oi.make_prefill_case(lens, 16, 8, 128, seed=5)
+    q, k, v, cu = c.q.to(gpu), c.k.to(gpu), c.v.to(gpu), c.cu_seqlens.to(gpu)
+    announce(f"prefill max_seqlen bound lens={lens}")
+    outs = [flash_attention_prefill(q, k, v, cu, c.scale, 16, 8, 128, max_seqlen=m)
+            for m in (max(lens), None, 4 * max(lens) + 3)]
+    torch.cuda.synchronize()
+    assert torch.equal(outs[0], outs[1]) and torch.equal(outs[0], outs[2])
+
+
 def test_prefill_batched_adaptor_pads_zero(gpu):
     """flash_attention_prefill_batched on a right-padded batch: valid rows
     match the closed form, pad rows are zero (reference :252-258)."""
