@@ -25,8 +25,9 @@
 //  * The S^T accumulator layout (lane = q column + 16*(token/4)) is exactly
 //    the B-operand layout of the PV product, so P goes to the matrix cores
 //    with no cross-lane traffic: O^T(128 x 16) = V^T(128 x 16 tok) P^T as
-//    8 x mfma_f32_16x16x16_bf16, where the V^T operand is built in-lane
-//    from the row-major 16-byte V loads with byte permutes.
+//    8 x 2 mfma_f32_16x16x16_bf16 (P split into bf16 hi + lo terms), where
+//    the V^T operand is built in-lane from the row-major 16-byte V loads
+//    with byte permutes.
 //  * Online softmax in the exp2 domain, one running max per query column,
 //    updated once per batch of tiles.
 //  * Batches above kStreamMaxB use a non-persistent grid variant (one
@@ -199,7 +200,11 @@ __device__ __forceinline__ void compute_chunk(Chunk& c, float scale_log2, int hi
   const float alpha = q3::fast_exp2(st.m - m_use);
   st.m = m_new;
 
-  q3::bf16x4 p[kChunk];
+  // P in fp32 as two bf16 terms, p = hi + lo (hi = bf16(p), lo = bf16(p -
+  // hi)): 16 significant bits, so V^T P^T carries P at about the fp32
+  // precision of the reference's product (the two MFMAs per step cost no
+  // time in this memory-bound loop).
+  q3::bf16x4 p[kChunk], pl[kChunk];
   float psum = 0.f;
 #pragma unroll
   for (int i = 0; i < kChunk; ++i) {
@@ -209,8 +214,14 @@ __device__ __forceinline__ void compute_chunk(Chunk& c, float scale_log2, int hi
       e[r] = q3::fast_exp2(s[i][r] - m_use);
       psum += e[r];
     }
-    q3::u32x2 pk = {q3::pack_bf16x2(e[0], e[1]), q3::pack_bf16x2(e[2], e[3])};
+    const q3::u32x2 pk = {q3::pack_bf16x2(e[0], e[1]), q3::pack_bf16x2(e[2], e[3])};
     p[i] = q3::as_bf16x4(pk);
+    // the rounded terms back in fp32: a bf16's bits are the top half of a float's
+    const float h0 = __uint_as_float(pk[0] << 16), h1 = __uint_as_float(pk[0] & 0xffff0000u);
+    const float h2 = __uint_as_float(pk[1] << 16), h3 = __uint_as_float(pk[1] & 0xffff0000u);
+    const q3::u32x2 lk = {q3::pack_bf16x2(e[0] - h0, e[1] - h1),
+                          q3::pack_bf16x2(e[2] - h2, e[3] - h3)};
+    pl[i] = q3::as_bf16x4(lk);
   }
   st.l = st.l * alpha + psum;
 #pragma unroll
@@ -228,6 +239,7 @@ __device__ __forceinline__ void compute_chunk(Chunk& c, float scale_log2, int hi
         q3::u32x2 av = {q3::pick_halves(c.v[i][0][w], c.v[i][1][w], h),
                         q3::pick_halves(c.v[i][2][w], c.v[i][3][w], h)};
         st.acc[j] = q3::mfma16x16x16(q3::as_bf16x4(av), p[i], st.acc[j]);
+        st.acc[j] = q3::mfma16x16x16(q3::as_bf16x4(av), pl[i], st.acc[j]);
       }
     }
   }
