@@ -109,6 +109,44 @@ def time_steps(fn, steps, warmup):
     return wall, evt
 
 
+def warm_up(fn, seconds=0.3):
+    """Runs fn (untimed) for about `seconds` of wall time, so the clocks
+    have ramped up before a short kernel is timed (its first tens of calls
+    after idle run up to ~10% slower)."""
+    import torch
+
+    t0 = time.perf_counter()
+    while time.perf_counter() - t0 < seconds:
+        for _ in range(10):
+            fn()
+        torch.cuda.synchronize()
+
+
+def time_graph(fn, steps, warmup):
+    """Back-to-back rate of a short kernel without the host's launch cost:
+    `steps` calls of fn captured into one HIP graph (after `warmup` eager
+    calls), replayed once untimed and then timed by one event pair on
+    torch's current stream around three replays.  Returns ms per call."""
+    import torch
+
+    for _ in range(max(warmup, 1)):
+        fn()
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        for _ in range(steps):
+            fn()
+    g.replay()
+    torch.cuda.synchronize()
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    start.record()
+    for _ in range(3):
+        g.replay()
+    end.record()
+    torch.cuda.synchronize()
+    return start.elapsed_time(end) / (3 * steps)
+
+
 _FLUSH = {}
 
 
@@ -147,6 +185,25 @@ def time_steps_flushed(fn, steps, warmup, dev):
         b.record()
     torch.cuda.synchronize()
     return sum(a.elapsed_time(b) for a, b in evs) / steps
+
+
+def copy_reference(nbytes, dev, steps, warmup):
+    """What a plain device copy (torch's copy kernel, nbytes / 2 read and
+    nbytes / 2 written, contiguous) reaches at the same size: GB/s after a
+    cache flush and back to back.  The ceiling a kernel of that many bytes
+    is measured against."""
+    import torch
+
+    n = nbytes // 4
+    src = torch.ones(n // 2, dtype=torch.int32, device=dev)
+    dst = torch.empty_like(src)
+    fn = lambda: dst.copy_(src)  # noqa: E731
+    warm_up(fn)
+    cold = time_steps_flushed(fn, steps, warmup, dev)
+    hot = time_graph(fn, steps, warmup)
+    b = 2 * src.numel() * 4
+    return {"GB/s_flushed": round(b / (cold * 1e-3) / 1e9, 1),
+            "GB/s_back_to_back": round(b / (hot * 1e-3) / 1e9, 1)}
 
 
 def seeded_lengths(n: int, lo: int, hi: int, seed: int = 0) -> list:
@@ -381,8 +438,9 @@ def bench_pre_attention(args, dev):
     def pstep():
         qk_norm_rope_prefill(q, k, v, w, w, 1e-6, cos, sin, pos, slots, kb, vb, 0, qo, ko)
 
+    warm_up(pstep)
     p_evt = time_steps_flushed(pstep, args.steps, args.warmup, dev)
-    _, p_hot = time_steps(pstep, args.steps, args.warmup)
+    p_hot = time_graph(pstep, args.steps, args.warmup)
     # per token: q, k, v read, one cos and one sin row, position + slot;
     # q_out, k_out, pool k and pool v written
     pbytes = T * ((hq + 2 * hkv) * 256 + 2 * 128 * 4 + 16 + (hq + 3 * hkv) * 256)
@@ -393,6 +451,8 @@ def bench_pre_attention(args, dev):
                       "ms_per_step": round(p_evt, 5), "ms_per_step_back_to_back": round(p_hot, 5),
                       "bytes": pbytes, "GB/s": round(gbs, 1),
                       "frac_hbm_peak": round(gbs / HBM_PEAK_GBS, 4),
+                      "GB/s_back_to_back": round(pbytes / (p_hot * 1e-3) / 1e9, 1),
+                      "copy_same_bytes": copy_reference(pbytes, dev, args.steps, args.warmup),
                       "traffic": profiled_traffic(PRE_ATTENTION_PROFILE),
                       "traffic_source": f"profiles/{PRE_ATTENTION_PROFILE}"}
     del qkv, q, k, v, kb, vb, qo, ko
@@ -464,12 +524,14 @@ def bench_prefill(args, dev):
             flash_attention_prefill(q, k, v, cu, 128 ** -0.5, 16, 8, 128, max_seqlen=4096,
                                     causal=False, out=out)
 
-        _, s_evt = time_steps(sstep, args.steps, args.warmup)
+        warm_up(sstep)
+        s_evt = time_graph(sstep, args.steps, args.warmup)
         flops = 4 * 128 * 16 * sum(L * L for L in lens)
         tflops = flops / (s_evt * 1e-3) / 1e12
         log(f"prefill (steady, 8x4096 non-causal): {s_evt * 1e3:.1f} us/call, {tflops:.1f} TFLOP/s")
         return {"workload": "varlen non-causal prefill, 8 x 4096 tokens, 16/8 heads, head_dim 128, bf16",
                 "value": round(tflops, 2), "unit": "TFLOP/s", "ms_per_step": round(s_evt, 5),
+                "timing": "graph replay of back-to-back calls, HIP events",
                 "flops": flops,
                 "roofline": {"bound": "mfma", "achieved": round(tflops, 2),
                              "peak": MFMA_BF16_PEAK_TFLOPS, "unit": "TFLOP/s",
@@ -500,14 +562,18 @@ def bench_prefill(args, dev):
         flash_attention_prefill(q, k, v, cu, scale, 16, 8, 128, max_seqlen=mx, out=out)
 
     # MFMA-bound: the line is the back-to-back rate (in a prefill its inputs
-    # come straight from the pre-attention kernel); the rate with q/k/v
-    # flushed out of the caches before every call rides along.
-    _, evt_ms = time_steps(step, args.steps, args.warmup)
+    # come straight from the pre-attention kernel), timed as a graph replay
+    # so the host's per-call launch cost (Python wrapper + ctypes, as much as
+    # the kernel itself) is not in it; the eager loop's rate and the rate
+    # with q/k/v flushed out of the caches before every call ride along.
+    warm_up(step)
+    evt_ms = time_graph(step, args.steps, args.warmup)
+    _, eager_ms = time_steps(step, args.steps, args.warmup)
     cold_ms = time_steps_flushed(step, args.steps, args.warmup, dev)
     flops = 2 * 128 * 16 * sum(L * (L + 1) for L in lens)
     tflops = flops / (evt_ms * 1e-3) / 1e12
-    log(f"prefill: {evt_ms * 1e3:.1f} us/call back to back ({cold_ms * 1e3:.1f} flushed), "
-        f"{tflops:.1f} TFLOP/s")
+    log(f"prefill: {evt_ms * 1e3:.1f} us/call back to back ({cold_ms * 1e3:.1f} flushed, "
+        f"{eager_ms * 1e3:.1f} eager loop), {tflops:.1f} TFLOP/s")
 
     # slot write of the same prefill into a block-16 pool (one launch), through
     # a seeded random slot mapping over 1.25x the blocks needed
@@ -525,8 +591,9 @@ def bench_prefill(args, dev):
             16, _lib.stream_of(dev))
         _lib.check(rc, "slots")
 
+    warm_up(wstep)
     w_evt = time_steps_flushed(wstep, args.steps, args.warmup, dev)
-    _, w_hot = time_steps(wstep, args.steps, args.warmup)
+    w_hot = time_graph(wstep, args.steps, args.warmup)
     wbytes = 8 * T * 8 * 128 + 8 * T
     wgbs = wbytes / (w_evt * 1e-3) / 1e9
     log(f"prefill slot write ({T} tokens): {w_evt * 1e3:.1f} us/call flushed "
@@ -534,7 +601,9 @@ def bench_prefill(args, dev):
     res = {"workload": f"varlen causal prefill, Qwen3-0.6B shape: 8 seqs lens={lens}, "
                        "16/8 heads, head_dim 128, bf16",
            "value": round(tflops, 2), "unit": "TFLOP/s", "ms_per_step": round(evt_ms, 5),
-           "ms_per_step_flushed": round(cold_ms, 5), "flops": flops,
+           "timing": "graph replay of back-to-back calls, HIP events",
+           "ms_per_step_flushed": round(cold_ms, 5),
+           "ms_per_step_eager_loop": round(eager_ms, 5), "flops": flops,
            "roofline": {"bound": "mfma", "achieved": round(tflops, 2),
                         "peak": MFMA_BF16_PEAK_TFLOPS, "unit": "TFLOP/s",
                         "frac": round(tflops / MFMA_BF16_PEAK_TFLOPS, 4),
@@ -542,7 +611,10 @@ def bench_prefill(args, dev):
                         "traffic_source": f"profiles/{PREFILL_PROFILE}"},
            "slot_write": {"GB/s": round(wgbs, 1), "frac_hbm_peak": round(wgbs / HBM_PEAK_GBS, 4),
                           "ms_per_step": round(w_evt, 5),
-                          "ms_per_step_back_to_back": round(w_hot, 5), "bytes": wbytes}}
+                          "ms_per_step_back_to_back": round(w_hot, 5), "bytes": wbytes,
+                          "GB/s_back_to_back": round(wbytes / (w_hot * 1e-3) / 1e9, 1),
+                          "copy_same_bytes": copy_reference(wbytes, dev, args.steps,
+                                                            args.warmup)}}
     if not args.no_cpu_baseline:
         res["cpu_baseline"] = cpu_baseline_prefill(lens, q, k, v, flops)
     return res
