@@ -87,6 +87,58 @@ __global__ __launch_bounds__(256) void kv_write_kernel(KvWriteArgs a) {
   }
 }
 
+// The same copy when a head row is 2^lc 16-byte chunks and one item (2 H
+// rows) is 2^li <= 256 chunks: a 256-thread workgroup moves 256 >> li whole
+// items and every index is a shift, not a 64-bit division (the division
+// otherwise costs as much issue time as the copy's memory traffic).
+template <Form F>
+__global__ __launch_bounds__(256) void kv_write_pow2_kernel(KvWriteArgs a, int lc, int li) {
+  const int tid = threadIdx.x;
+  const int64_t item = (static_cast<int64_t>(blockIdx.x) << (8 - li)) + (tid >> li);
+  if (item >= a.n_items) return;
+  const int rem = tid & ((1 << li) - 1);
+  const int c = rem & ((1 << lc) - 1);
+  const int is_v = (rem >> lc) & 1;
+  const int h = rem >> (lc + 1);
+
+  int64_t phys, off;
+  if constexpr (F == Form::Decode) {
+    const int64_t row = a.row_ids ? a.row_ids[item] : item;
+    if (row < 0 || row >= a.max_rows) return;
+    const int64_t pos = a.seq_lens[row];
+    if (pos < 0) return;
+    const int64_t pg = pos / a.bs;
+    if (pg >= a.max_pages) return;
+    phys = a.block_table[row * a.bt_stride + pg];
+    off = pos % a.bs;
+  } else if constexpr (F == Form::Range) {
+    const int64_t pos = a.start_pos + item;
+    const int64_t pg = pos / a.bs;
+    if (pos < 0 || pg >= a.max_pages) return;
+    phys = a.block_table[pg];
+    off = pos % a.bs;
+  } else {
+    const int64_t slot = a.slots[item];
+    if (slot < 0) return;
+    phys = slot / a.bs;
+    off = slot % a.bs;
+  }
+  if (phys < 0 || phys >= a.num_blocks) return;
+  const uint16_t* src = is_v ? a.v_new + item * a.vn_s0 + h * a.vn_s1
+                             : a.k_new + item * a.kn_s0 + h * a.kn_s1;
+  const int64_t* cs = is_v ? a.vc : a.kc;
+  uint16_t* dst = (is_v ? a.v_cache : a.k_cache) + phys * cs[0] +
+                  static_cast<int64_t>(a.layer) * cs[1] + h * cs[2] + off * cs[3];
+  q3::st16(dst + c * 8, q3::ld16(src + c * 8));
+}
+
+int log2_exact(int64_t x) {  // -1 unless x is a power of two
+  if (x <= 0 || (x & (x - 1))) return -1;
+  int l = 0;
+  while ((int64_t{1} << l) < x) ++l;
+  return l;
+}
+
 // Validates the arguments shared by the three forms and picks the vector
 // width: 16-byte chunks when every base pointer and stride keeps 16-byte
 // alignment, element copies otherwise.
@@ -120,7 +172,11 @@ int launch(const KvWriteArgs& a, void* stream, const char* who) {
   if (blocks > 0x7fffffff) return q3::fail(QWEN3_EINVAL, "%s: too many tokens", who);
   q3::clear_error();
   hipStream_t s = static_cast<hipStream_t>(stream);
-  if (vec16)
+  const int lc = log2_exact(a.D / 8), li = log2_exact(2 * static_cast<int64_t>(a.H) * (a.D / 8));
+  if (vec16 && lc >= 0 && li >= 0 && li <= 8) {
+    const int64_t wgs = q3::cdiv(a.n_items, int64_t{1} << (8 - li));
+    hipLaunchKernelGGL((kv_write_pow2_kernel<F>), dim3(wgs), dim3(256), 0, s, a, lc, li);
+  } else if (vec16)
     hipLaunchKernelGGL((kv_write_kernel<F, 8>), dim3(blocks), dim3(256), 0, s, a);
   else
     hipLaunchKernelGGL((kv_write_kernel<F, 1>), dim3(blocks), dim3(256), 0, s, a);
