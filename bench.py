@@ -206,6 +206,28 @@ def copy_reference(nbytes, dev, steps, warmup):
             "GB/s_back_to_back": round(b / (hot * 1e-3) / 1e9, 1)}
 
 
+def read_reference(nbytes, dev, reps=5):
+    """What torch's own streaming reduction (a max over an int64 buffer of
+    nbytes) reads per second: a plain full-device read of the decode call's
+    byte count, the reference point of the decode line."""
+    import torch
+
+    buf = torch.ones(nbytes // 8, dtype=torch.int64, device=dev)
+    torch.amax(buf)
+    torch.cuda.synchronize()
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    start.record()
+    for _ in range(reps):
+        torch.amax(buf)
+    end.record()
+    torch.cuda.synchronize()
+    ms = start.elapsed_time(end) / reps
+    del buf
+    torch.cuda.empty_cache()
+    return {"GB/s": round(nbytes / (ms * 1e-3) / 1e9, 1), "ms": round(ms, 5),
+            "kernel": f"torch.amax over {nbytes} bytes of int64"}
+
+
 def seeded_lengths(n: int, lo: int, hi: int, seed: int = 0) -> list:
     """n lengths uniform in [lo, hi] from a seeded CPU generator."""
     import torch
@@ -850,8 +872,10 @@ def main(argv=None):
                             "traffic_source": f"profiles/{TRAFFIC_PROFILE}" if traffic else None}
         if not args.no_cpu_baseline:
             line["cpu_baseline"] = cpu_baseline_decode(res, args.cpu_sample)
+        nbytes = res["bytes"]
         del res
         torch.cuda.empty_cache()
+        line["roofline"]["read_reference"] = read_reference(nbytes, dev)
         if args.workload == "config3" and not args.no_long_context:
             long_args = argparse.Namespace(**{**vars(args), "workload": "config4"})
             r4 = bench_decode(long_args, dev)
