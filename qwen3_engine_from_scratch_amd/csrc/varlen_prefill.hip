@@ -516,18 +516,36 @@ __device__ __forceinline__ void prefill_item(const PrefillArgs& a, const LaneOff
   }
 
   l_run = cross_half_sum(l_run);
-  if (!wave_active || qrow >= len) return;
-  const float inv = l_run > 0.f ? 1.f / l_run : 0.f;
-  uint16_t* op = a.o + (start + qrow) * a.o_st + static_cast<int64_t>(head) * a.o_sh;
+  if (!wave_active) return;
+  // The output goes through LDS so that each global store writes whole
+  // 256-byte rows (four per instruction) instead of 16 bytes of 32 rows:
+  // every tile buffer is free after the loop's last barrier, and the
+  // caller's barrier follows before the next item's loads refill them.
+  // Wave w stages its 32 x 128 tile in 8 KiB of buffer w / 2, chunk c of
+  // row r at chunk c ^ (r % 16) (conflict-free for both directions).
+  const float inv = l_run > 0.f ? 1.f / l_run : 0.f;  // 0 for rows past the end
+  const int sb = wave >> 1;
+  char* stage = reinterpret_cast<char*>(sb == 0 ? tb.k0 : sb == 1 ? tb.v0 : sb == 2 ? tb.k1 : tb.v1) +
+                (wave & 1) * 8192;
 #pragma unroll
   for (int db = 0; db < 4; ++db)
 #pragma unroll
     for (int g4 = 0; g4 < 4; ++g4) {
-      const int d = 32 * db + 8 * g4 + 4 * hl;
+      const int ch = 4 * db + g4;
       q3::u32x2 w = {q3::pack_bf16x2(acc[db][4 * g4] * inv, acc[db][4 * g4 + 1] * inv),
                      q3::pack_bf16x2(acc[db][4 * g4 + 2] * inv, acc[db][4 * g4 + 3] * inv)};
-      *reinterpret_cast<q3::u32x2*>(op + d) = w;
+      *reinterpret_cast<q3::u32x2*>(stage + l32 * 256 + ((ch ^ (l32 & 15)) << 4) + hl * 8) = w;
     }
+  const int oc = lane & 15;  // this lane's 16-byte chunk of a row
+#pragma unroll
+  for (int j = 0; j < 8; ++j) {
+    const int rr = 4 * j + (lane >> 4);
+    const q3::u32x4 v =
+        *reinterpret_cast<const q3::u32x4*>(stage + rr * 256 + ((oc ^ (rr & 15)) << 4));
+    const int row = q0 + rr;
+    if (row < len)
+      q3::st16(a.o + (start + row) * a.o_st + static_cast<int64_t>(head) * a.o_sh + oc * 8, v);
+  }
 }
 
 // The four staged tile buffers, as separate LDS arrays so loads into one
