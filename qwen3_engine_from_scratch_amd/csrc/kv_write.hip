@@ -89,8 +89,9 @@ __global__ __launch_bounds__(256) void kv_write_kernel(KvWriteArgs a) {
 
 // The same copy when a head row is 2^lc 16-byte chunks and one item (2 H
 // rows) is 2^li <= 256 chunks: a 256-thread workgroup moves 256 >> li whole
-// items and every index is a shift, not a 64-bit division (the division
-// otherwise costs as much issue time as the copy's memory traffic).
+// items and every index is a shift instead of the general kernel's 64-bit
+// division per chunk (the 66.5 MB write of an 8,115-token prefill: 13.9 ->
+// 13.4 us back to back).
 template <Form F>
 __global__ __launch_bounds__(256) void kv_write_pow2_kernel(KvWriteArgs a, int lc, int li) {
   const int tid = threadIdx.x;

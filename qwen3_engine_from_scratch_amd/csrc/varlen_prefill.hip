@@ -265,8 +265,9 @@ __device__ __forceinline__ void save_partial(__amdgpu_buffer_rsrc_t slot, int wa
   __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(l_run), slot, ml + 4, 0, kCpolDevice);
 }
 
-// Folds the other part's saved state into st (both relative to their own
-// running max; the result is relative to the larger one).  The sums are
+// Folds the other part's saved state into (m_run, l_run, acc) (both
+// relative to their own running max; the result is relative to the larger
+// one).  The sums are
 // formed as part 0 * its weight + part 1 * its weight whichever part merges,
 // so the output does not depend on which part finished first.
 __device__ __forceinline__ void merge_partial(__amdgpu_buffer_rsrc_t slot, int wave, int lane,
