@@ -61,6 +61,7 @@ struct PreAttnArgs {
   const int64_t* slots;
   int64_t n_tokens;
   int Hq, Hkv, bs;
+  int gpt_shift;  // log2 of the groups per token when a power of two, else -1
 };
 
 __device__ __forceinline__ float bf_lo(uint32_t w) { return __uint_as_float(w << 16); }
@@ -78,14 +79,21 @@ template <Addr A>
 __global__ __launch_bounds__(256) void pre_attention_kernel(PreAttnArgs a) {
   const int hr_count = a.Hq + 2 * a.Hkv;
   const int groups_per_token = (hr_count + kRowsPerGroup - 1) / kRowsPerGroup;
-  const int64_t g = static_cast<int64_t>(blockIdx.x) * kGroupsPerBlock + (threadIdx.x >> 4);
-  if (g >= a.n_tokens * groups_per_token) return;  // whole 16-lane groups leave together
+  // 32-bit group index (the host keeps tokens x groups below 2^31): a shift
+  // or a 32-bit division instead of a 64-bit one.
+  const uint32_t g = blockIdx.x * kGroupsPerBlock + (threadIdx.x >> 4);
+  if (g >= static_cast<uint32_t>(a.n_tokens * groups_per_token)) return;  // whole groups leave
   const int j = threadIdx.x & (kLanesPerRow - 1);
-  const int64_t t = g / groups_per_token;
-  const int hr0 = static_cast<int>(g - t * groups_per_token) * kRowsPerGroup;
+  const uint32_t t32 = a.gpt_shift >= 0 ? g >> a.gpt_shift : g / groups_per_token;
+  const int64_t t = t32;
+  const int hr0 = static_cast<int>(g - t32 * groups_per_token) * kRowsPerGroup;
   const int nrows = min(kRowsPerGroup, hr_count - hr0);
 
   // This group's head rows first (independent of the position lookups).
+  // The token's row bases are formed once; a row adds its head offset.
+  const uint16_t* q_tok = a.q + t * a.q_s0;
+  const uint16_t* k_tok = a.k + t * a.k_s0;
+  const uint16_t* v_tok = a.v + t * a.v_s0;
   q3::u32x4 xw[kRowsPerGroup], ww[kRowsPerGroup];
 #pragma unroll
   for (int i = 0; i < kRowsPerGroup; ++i) {
@@ -93,13 +101,13 @@ __global__ __launch_bounds__(256) void pre_attention_kernel(PreAttnArgs a) {
     if (i >= nrows) break;
     const uint16_t* src;
     if (hr < a.Hq) {
-      src = a.q + t * a.q_s0 + hr * a.q_s1;
+      src = q_tok + hr * a.q_s1;
       ww[i] = q3::ld16(a.q_w + 8 * j);
     } else if (hr < a.Hq + a.Hkv) {
-      src = a.k + t * a.k_s0 + (hr - a.Hq) * a.k_s1;
+      src = k_tok + (hr - a.Hq) * a.k_s1;
       ww[i] = q3::ld16(a.k_w + 8 * j);
     } else {
-      src = a.v + t * a.v_s0 + (hr - a.Hq - a.Hkv) * a.v_s1;
+      src = v_tok + (hr - a.Hq - a.Hkv) * a.v_s1;
     }
     xw[i] = q3::ld16(src + 8 * j);
   }
@@ -129,6 +137,8 @@ __global__ __launch_bounds__(256) void pre_attention_kernel(PreAttnArgs a) {
   // (and its q/k rows zero).
   const bool ok_pos = pos >= 0 && pos < a.tab_rows;
   const bool write_pool = ok_pos && phys >= 0 && phys < a.num_blocks;
+  const int64_t kc_tok = phys * a.kc[0] + static_cast<int64_t>(a.layer) * a.kc[1] + off * a.kc[3];
+  const int64_t vc_tok = phys * a.vc[0] + static_cast<int64_t>(a.layer) * a.vc[1] + off * a.vc[3];
 
   float cv[8], sv[8];
   if (ok_pos && hr0 < a.Hq + a.Hkv) {
@@ -146,7 +156,13 @@ __global__ __launch_bounds__(256) void pre_attention_kernel(PreAttnArgs a) {
       sv[e] = round_bf16(ss_[e]);
     }
   }
-  const float sign = j < kLanesPerRow / 2 ? -1.f : 1.f;  // rotate_half: (-x2, x1)
+  // rotate_half: (-x2, x1).  The sign goes into this lane's sin values once
+  // (sign * p * s == p * (sign * s) exactly).
+  {
+    const float sign = j < kLanesPerRow / 2 ? -1.f : 1.f;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) sv[e] *= sign;
+  }
 
 #pragma unroll
   for (int i = 0; i < kRowsPerGroup; ++i) {
@@ -154,9 +170,7 @@ __global__ __launch_bounds__(256) void pre_attention_kernel(PreAttnArgs a) {
     const int hr = hr0 + i;
     if (hr >= a.Hq + a.Hkv) {  // v row: bit-exact copy into the pool
       if (write_pool)
-        q3::st16(a.v_cache + phys * a.vc[0] + static_cast<int64_t>(a.layer) * a.vc[1] +
-                     (hr - a.Hq - a.Hkv) * a.vc[2] + off * a.vc[3] + 8 * j,
-                 xw[i]);
+        q3::st16(a.v_cache + vc_tok + (hr - a.Hq - a.Hkv) * a.vc[2] + 8 * j, xw[i]);
       continue;
     }
     float x[8], w[8];
@@ -173,6 +187,8 @@ __global__ __launch_bounds__(256) void pre_attention_kernel(PreAttnArgs a) {
     for (int e = 0; e < 8; ++e) ss = __fadd_rn(ss, __fmul_rn(x[e], x[e]));
 #pragma unroll
     for (int m = 1; m < kLanesPerRow; m <<= 1) ss += __shfl_xor(ss, m, kLanesPerRow);
+    // 1 / sqrt with IEEE sqrt and division: the hardware rsqrt's extra ulp
+    // moves some outputs by two bf16 ulps from the reference's rsqrt.
     const float rms = 1.f / sqrtf(ss / static_cast<float>(kD) + a.eps);
 
     // n = bf16((x * rms) * w), packed as bf16 pairs for the partner exchange.
@@ -188,15 +204,11 @@ __global__ __launch_bounds__(256) void pre_attention_kernel(PreAttnArgs a) {
     if (ok_pos) {
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
-        float o[2];
-#pragma unroll
-        for (int hlf = 0; hlf < 2; ++hlf) {
-          const int el = 2 * e + hlf;
-          const float n = hlf ? bf_hi(np[e]) : bf_lo(np[e]);
-          const float rh = sign * (hlf ? bf_hi(pp[e]) : bf_lo(pp[e]));
-          o[hlf] = round_bf16(n * cv[el]) + round_bf16(rh * sv[el]);
-        }
-        out[e] = q3::pack_bf16x2(o[0], o[1]);
+        // bf16(n * c) and bf16(rotate_half(n) * s) for elements 2e, 2e + 1,
+        // each pair rounded by one packed conversion
+        const uint32_t nc = q3::pack_bf16x2(bf_lo(np[e]) * cv[2 * e], bf_hi(np[e]) * cv[2 * e + 1]);
+        const uint32_t rs = q3::pack_bf16x2(bf_lo(pp[e]) * sv[2 * e], bf_hi(pp[e]) * sv[2 * e + 1]);
+        out[e] = q3::pack_bf16x2(bf_lo(nc) + bf_lo(rs), bf_hi(nc) + bf_hi(rs));
       }
     }
     if (hr < a.Hq) {
@@ -205,10 +217,7 @@ __global__ __launch_bounds__(256) void pre_attention_kernel(PreAttnArgs a) {
     }
     const int h = hr - a.Hq;
     if (a.k_out) q3::st16(a.k_out + t * a.ko_s0 + h * a.ko_s1 + 8 * j, out);
-    if (write_pool)
-      q3::st16(a.k_cache + phys * a.kc[0] + static_cast<int64_t>(a.layer) * a.kc[1] +
-                   h * a.kc[2] + off * a.kc[3] + 8 * j,
-               out);
+    if (write_pool) q3::st16(a.k_cache + kc_tok + h * a.kc[2] + 8 * j, out);
   }
 }
 
@@ -240,12 +249,17 @@ int check_args(const PreAttnArgs& a, int head_dim, const char* who) {
 }
 
 template <Addr A>
-int launch(const PreAttnArgs& a, void* stream, const char* who) {
+int launch(PreAttnArgs a, void* stream, const char* who) {
   if (a.n_tokens == 0) return QWEN3_OK;
-  const int64_t groups =
-      a.n_tokens * ((a.Hq + 2 * a.Hkv + kRowsPerGroup - 1) / kRowsPerGroup);
+  const int gpt = (a.Hq + 2 * a.Hkv + kRowsPerGroup - 1) / kRowsPerGroup;
+  const int64_t groups = a.n_tokens * gpt;
+  // The kernel indexes 16-lane groups with 32-bit integers.
+  if (groups > 0x7fffffff - kGroupsPerBlock)
+    return q3::fail(QWEN3_EINVAL, "%s: too many tokens", who);
   const int64_t blocks = q3::cdiv(groups, kGroupsPerBlock);
-  if (blocks > 0x7fffffff) return q3::fail(QWEN3_EINVAL, "%s: too many tokens", who);
+  a.gpt_shift = -1;
+  for (int l = 0; l < 31; ++l)
+    if ((1 << l) == gpt) a.gpt_shift = l;
   q3::clear_error();
   hipLaunchKernelGGL(pre_attention_kernel<A>, dim3(static_cast<unsigned>(blocks)), dim3(256), 0,
                      static_cast<hipStream_t>(stream), a);
