@@ -169,7 +169,7 @@ def time_steps_flushed(fn, steps, warmup, dev):
     """For working sets under 512 MB: W untimed warmups, then K reps, each
     after a cache flush and between its own pair of HIP events on torch's
     current stream (the launch stream).  Returns event ms per rep (the
-    average of the K intervals); the flush itself is outside them."""
+    median of the K intervals); the flush itself is outside them."""
     import torch
 
     for _ in range(warmup):
@@ -184,7 +184,8 @@ def time_steps_flushed(fn, steps, warmup, dev):
         fn()
         b.record()
     torch.cuda.synchronize()
-    return sum(a.elapsed_time(b) for a, b in evs) / steps
+    ts = sorted(a.elapsed_time(b) for a, b in evs)
+    return ts[len(ts) // 2] if len(ts) % 2 else 0.5 * (ts[len(ts) // 2 - 1] + ts[len(ts) // 2])
 
 
 def copy_reference(nbytes, dev, steps, warmup):
