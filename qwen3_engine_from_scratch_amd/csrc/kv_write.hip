@@ -133,6 +133,58 @@ __global__ __launch_bounds__(256) void kv_write_pow2_kernel(KvWriteArgs a, int l
   q3::st16(dst + c * 8, q3::ld16(src + c * 8));
 }
 
+// One wave per item when an item is 64 x NPL chunks (NPL = 1, 2, 4, 8): the
+// item's slot is looked up once, and each lane issues its NPL loads before
+// its NPL stores, so a lane keeps NPL loads in flight (after a cache flush
+// the copy is bound by load latency, not by bandwidth).
+template <Form F, int NPL>
+__global__ __launch_bounds__(256) void kv_write_wave_kernel(KvWriteArgs a, int lc) {
+  const int lane = threadIdx.x & 63;
+  const int64_t item = static_cast<int64_t>(blockIdx.x) * 4 + (threadIdx.x >> 6);
+  if (item >= a.n_items) return;
+
+  int64_t phys, off;
+  if constexpr (F == Form::Decode) {
+    const int64_t row = a.row_ids ? a.row_ids[item] : item;
+    if (row < 0 || row >= a.max_rows) return;
+    const int64_t pos = a.seq_lens[row];
+    if (pos < 0) return;
+    const int64_t pg = pos / a.bs;
+    if (pg >= a.max_pages) return;
+    phys = a.block_table[row * a.bt_stride + pg];
+    off = pos % a.bs;
+  } else if constexpr (F == Form::Range) {
+    const int64_t pos = a.start_pos + item;
+    const int64_t pg = pos / a.bs;
+    if (pos < 0 || pg >= a.max_pages) return;
+    phys = a.block_table[pg];
+    off = pos % a.bs;
+  } else {
+    const int64_t slot = a.slots[item];
+    if (slot < 0) return;
+    phys = slot / a.bs;
+    off = slot % a.bs;
+  }
+  if (phys < 0 || phys >= a.num_blocks) return;
+  const uint16_t* k_src = a.k_new + item * a.kn_s0;
+  const uint16_t* v_src = a.v_new + item * a.vn_s0;
+  uint16_t* k_dst = a.k_cache + phys * a.kc[0] + static_cast<int64_t>(a.layer) * a.kc[1] + off * a.kc[3];
+  uint16_t* v_dst = a.v_cache + phys * a.vc[0] + static_cast<int64_t>(a.layer) * a.vc[1] + off * a.vc[3];
+  q3::u32x4 val[NPL];
+#pragma unroll
+  for (int k = 0; k < NPL; ++k) {
+    const int cc = lane + 64 * k;  // chunk of the item: (head, k/v, 16-byte chunk)
+    const int c = cc & ((1 << lc) - 1), is_v = (cc >> lc) & 1, h = cc >> (lc + 1);
+    val[k] = q3::ld16((is_v ? v_src + h * a.vn_s1 : k_src + h * a.kn_s1) + c * 8);
+  }
+#pragma unroll
+  for (int k = 0; k < NPL; ++k) {
+    const int cc = lane + 64 * k;
+    const int c = cc & ((1 << lc) - 1), is_v = (cc >> lc) & 1, h = cc >> (lc + 1);
+    q3::st16((is_v ? v_dst + h * a.vc[2] : k_dst + h * a.kc[2]) + c * 8, val[k]);
+  }
+}
+
 int log2_exact(int64_t x) {  // -1 unless x is a power of two
   if (x <= 0 || (x & (x - 1))) return -1;
   int l = 0;
@@ -174,7 +226,16 @@ int launch(const KvWriteArgs& a, void* stream, const char* who) {
   q3::clear_error();
   hipStream_t s = static_cast<hipStream_t>(stream);
   const int lc = log2_exact(a.D / 8), li = log2_exact(2 * static_cast<int64_t>(a.H) * (a.D / 8));
-  if (vec16 && lc >= 0 && li >= 0 && li <= 8) {
+  if (vec16 && lc >= 0 && li >= 6 && li <= 9) {
+    const int64_t wgs = q3::cdiv(a.n_items, int64_t{4});
+    if (wgs > 0x7fffffff) return q3::fail(QWEN3_EINVAL, "%s: too many tokens", who);
+    switch (li) {
+      case 6: hipLaunchKernelGGL((kv_write_wave_kernel<F, 1>), dim3(wgs), dim3(256), 0, s, a, lc); break;
+      case 7: hipLaunchKernelGGL((kv_write_wave_kernel<F, 2>), dim3(wgs), dim3(256), 0, s, a, lc); break;
+      case 8: hipLaunchKernelGGL((kv_write_wave_kernel<F, 4>), dim3(wgs), dim3(256), 0, s, a, lc); break;
+      default: hipLaunchKernelGGL((kv_write_wave_kernel<F, 8>), dim3(wgs), dim3(256), 0, s, a, lc); break;
+    }
+  } else if (vec16 && lc >= 0 && li >= 0 && li <= 8) {
     const int64_t wgs = q3::cdiv(a.n_items, int64_t{1} << (8 - li));
     hipLaunchKernelGGL((kv_write_pow2_kernel<F>), dim3(wgs), dim3(256), 0, s, a, lc, li);
   } else if (vec16)
