@@ -721,7 +721,9 @@ void varlen_prefill_persistent_kernel(PrefillArgs a) {
   // site of `run` costs registers in the tile loop).
   //  - static: round r takes item r * nwg + w, mirrored on odd rounds
   //    (w' = the same XCD, the opposite end of the CU order), which pairs
-  //    heavy items with light ones;
+  //    heavy items with light ones, and on a last round that does not
+  //    fill the grid (its items go to the workgroups whose first items
+  //    were the lightest, not to those holding the heaviest);
   //  - counters (eight-wave path, given a workspace): the first round is
   //    the static one; pool p holds the later items with i % 8 == p
   //    (ticket j is item nwg + j * 8 + p), a workgroup draws from the pool
@@ -777,7 +779,8 @@ void varlen_prefill_persistent_kernel(PrefillArgs a) {
     if (counters) {
       i = draw();
     } else {
-      i = static_cast<int64_t>(round) * nwg + ((round & 1) ? w_mirror : w);
+      const bool mirror = (round & 1) || static_cast<int64_t>(round + 1) * nwg > T;
+      i = static_cast<int64_t>(round) * nwg + (mirror ? w_mirror : w);
       if (i >= T) i = -1;
       __syncthreads();  // the item's LDS tiles are no longer read
     }
