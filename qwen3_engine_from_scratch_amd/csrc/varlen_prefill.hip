@@ -316,13 +316,9 @@ __device__ __forceinline__ void merge_partial(__amdgpu_buffer_rsrc_t slot, int w
 // Every thread of the workgroup calls it.
 template <int W, bool Split = false>
 __device__ __forceinline__ void prefill_item(const PrefillArgs& a, const LaneOffsets& off,
-                                             int seq, int hg, int mt, const TileBufs& tb,
-                                             int part = -1, int slot = 0,
+                                             int64_t start, int len, int hg, int mt,
+                                             const TileBufs& tb, int part = -1, int slot = 0,
                                              uint32_t* s_role = nullptr) {
-  const int64_t start = a.cu[seq];
-  const int64_t end = a.cu[seq + 1];
-  if (start < 0 || end > a.total || end <= start) return;
-  const int len = static_cast<int>(end - start);
   const int m0 = mt * a.rows;
   if (m0 >= len) return;
 
@@ -572,7 +568,10 @@ void varlen_prefill_flat_kernel(PrefillArgs a) {
   const int seq = static_cast<int>((id / a.groups) % a.num_seqs);
   const int mt =
       a.n_mtiles - 1 - static_cast<int>(id / (static_cast<int64_t>(a.groups) * a.num_seqs));
-  prefill_item<W>(a, off, seq, hg, mt, tb);
+  const int64_t start = a.cu[seq];
+  const int64_t end = a.cu[seq + 1];
+  if (start < 0 || end > a.total || end <= start) return;
+  prefill_item<W>(a, off, start, static_cast<int>(end - start), hg, mt, tb);
 }
 
 // Exclusive prefix sum over n <= kScanMax ints held in LDS (in place); returns
@@ -618,11 +617,11 @@ __device__ __forceinline__ int block_exclusive_scan(int* v, int n, int* s_wsum) 
 // the highest index first; within one, longest sequences first (ties by
 // index), head group fastest.  s_first[r] = items before query-tile rank r
 // (r = n_mtiles - 1 - mt); s_len[t] = sequence t's length (0 for a range
-// outside the batch).  Returns the number of items.  Called by all threads
+// outside the batch) and s_start[t] its first row.  Returns the number of items.  Called by all threads
 // of the workgroup.
 template <int W>
-__device__ __forceinline__ int build_items(const PrefillArgs& a, int* s_len, int* s_sorted,
-                                           int* s_first, int* s_wsum) {
+__device__ __forceinline__ int build_items(const PrefillArgs& a, int* s_len, int* s_start,
+                                           int* s_sorted, int* s_first, int* s_wsum) {
   const int tid = threadIdx.x;
   const int S = a.num_seqs;
   const int nm = a.n_mtiles;
@@ -630,6 +629,7 @@ __device__ __forceinline__ int build_items(const PrefillArgs& a, int* s_len, int
     const int64_t s0 = a.cu[t], s1 = a.cu[t + 1];
     const bool ok = s0 >= 0 && s1 <= a.total && s1 > s0;
     s_len[t] = ok ? static_cast<int>(s1 - s0) : 0;
+    s_start[t] = ok ? static_cast<int>(s0) : 0;
   }
   __syncthreads();
   // Rank by length, longest first (ties by index).
@@ -697,6 +697,7 @@ __attribute__((amdgpu_waves_per_eu(Q3_PREFILL_PERSISTENT_WAVES_PER_EU, Q3_PREFIL
 void varlen_prefill_persistent_kernel(PrefillArgs a) {
   Q3_PREFILL_TILE_BUFFERS;
   __shared__ int s_len[kMaxSeqs];
+  __shared__ int s_start[kMaxSeqs];
   __shared__ int s_sorted[kMaxSeqs];
   __shared__ int s_first[kScanMax];  // items before m-tile rank r (r = n_mtiles-1-mt)
   __shared__ int s_wsum[W];
@@ -710,12 +711,14 @@ void varlen_prefill_persistent_kernel(PrefillArgs a) {
     asm volatile("" ::"v"(prev));  // performed before this thread reaches the barriers below
   }
 
-  const int T = build_items<W>(a, s_len, s_sorted, s_first, s_wsum);
+  const int T = build_items<W>(a, s_len, s_start, s_sorted, s_first, s_wsum);
 
   auto run = [&](int64_t i64) {
     int seq, hg, mt;
     item_at(a, i64, s_first, s_sorted, seq, hg, mt);
-    prefill_item<W>(a, off, seq, hg, mt, tb);
+    // the sequence's rows from LDS, as scalars (no global load per item)
+    prefill_item<W>(a, off, __builtin_amdgcn_readfirstlane(s_start[seq]),
+                    __builtin_amdgcn_readfirstlane(s_len[seq]), hg, mt, tb);
   };
   // One loop and one inlined item body for both orders (each extra call
   // site of `run` costs registers in the tile loop).
@@ -912,13 +915,14 @@ __global__ __launch_bounds__(W * 64) __attribute__((amdgpu_waves_per_eu(2, 2)))
 void varlen_prefill_split_kernel(PrefillArgs a) {
   Q3_PREFILL_TILE_BUFFERS;
   __shared__ int s_len[kMaxSeqs];
+  __shared__ int s_start[kMaxSeqs];
   __shared__ int s_sorted[kMaxSeqs];
   __shared__ int s_first[kScanMax];  // items before m-tile rank r (r = n_mtiles-1-mt)
   __shared__ int s_cls[kScanMax];    // entries before work class 2 n_mtiles - j
   __shared__ int s_wsum[W];
   __shared__ unsigned long long s_work;
   __shared__ uint32_t s_role;
-  const int T_items = build_items<W>(a, s_len, s_sorted, s_first, s_wsum);
+  const int T_items = build_items<W>(a, s_len, s_start, s_sorted, s_first, s_wsum);
   const SplitPlan plan =
       plan_splits<W>(a, s_len, s_first, T_items, gridDim.x, s_cls, s_wsum, &s_work);
   const int64_t nwg = gridDim.x;
@@ -928,7 +932,9 @@ void varlen_prefill_split_kernel(PrefillArgs a) {
   for (int round = 1; i < plan.E; ++round) {
     int seq, hg, mt, part, slot;
     entry_at(a, plan, i, s_first, s_sorted, s_cls, seq, hg, mt, part, slot);
-    prefill_item<W, true>(a, off, seq, hg, mt, tb, part, slot, &s_role);
+    const int64_t start = a.cu[seq];  // a valid range: the entry exists
+    prefill_item<W, true>(a, off, start, static_cast<int>(a.cu[seq + 1] - start), hg, mt, tb,
+                          part, slot, &s_role);
     i = static_cast<int64_t>(round) * nwg + ((round & 1) ? w_mirror : w);
     __syncthreads();  // the entry's LDS tiles are no longer read
   }
