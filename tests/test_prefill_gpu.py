@@ -95,6 +95,19 @@ def test_prefill_large_batches_vs_fp32(gpu, lens, hq, hkv, causal):
     assert_close_attn(out, _gpu_ref_fp32(c, gpu, hq // hkv, causal), f"lens={lens}")
 
 
+@pytest.mark.parametrize("lens", [
+    [1215, 1488, 90, 1096, 641, 307, 1395, 1001, 1321, 540, 1453, 201],  # last round partial
+    [2048, 2048, 2048, 2048],  # 1,024 items: two full rounds of 512 workgroups
+])
+def test_prefill_four_wave_rounds_vs_fp32(gpu, lens):
+    """Four-wave workgroups in the static order over several rounds (a last
+    round that does not fill the grid goes in the mirrored order)."""
+    c = oi.make_prefill_case(lens, 16, 8, 128, seed=len(lens))
+    announce(f"prefill four-wave rounds lens={lens}")
+    out = _run(c, gpu, 16, 8)
+    assert_close_attn(out, _gpu_ref_fp32(c, gpu, 2), f"lens={lens}")
+
+
 def test_prefill_strided_views_of_fused_qkv(gpu):
     """q, k and v as head slices of one fused (T, 32, 128) projection (row
     stride 4096 elements) and the output into a slice of a wider buffer: the
