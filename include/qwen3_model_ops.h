@@ -40,6 +40,8 @@
  *                              fused top-p / Gumbel-max kernel of its fast path
  *                              (:112-178) and its torch fallback (:76-108):
  *                              temperature, top-k, top-p per row in one launch
+ *   qwen3_sample_ws_bf16    <- the same sample_tokens, its row-streaming
+ *                              passes spread over parallel workgroups
  *   qwen3_advance_seq_lens  <- the resident-length write of
  *                              PagedKVCache.advance_seq_len
  *                              (qwen3/PagedKVcache.py:216-219), one launch for
@@ -171,6 +173,23 @@ int qwen3_page_in_bf16(int32_t* block_table, int64_t bt_row_stride, int64_t max_
 int qwen3_sample_bf16(const void* logits, int64_t row_stride, int64_t rows, int64_t vocab,
                       const float* temperature, const int32_t* top_k, const float* top_p,
                       uint64_t seed, int64_t* out, void* stream);
+
+/* qwen3_sample_bf16's draws, bit for bit, for batches too small to fill the
+ * CUs with one workgroup per row (<= 128 rows): each row is split over 2-8
+ * parts (8 for <= 32 rows, 4 for <= 64, 2 for <= 128, at most one per
+ * 8,192 tokens); a workgroup per part finds the part's own top-k boundary
+ * and keeps the tokens at or above it, and a second launch draws from the
+ * union of those lists (it holds every token of the row's top k), falling
+ * back to streaming the row when the lists overflow.  The launches meet in
+ * a caller workspace of qwen3_sample_workspace_bytes(rows, vocab) bytes
+ * (device, 16-byte aligned, no initialisation; calls that share one must
+ * not overlap); 0 bytes means one part per row, and then, or with a NULL
+ * workspace, this call is qwen3_sample_bf16. */
+size_t qwen3_sample_workspace_bytes(int64_t rows, int64_t vocab);
+int qwen3_sample_ws_bf16(const void* logits, int64_t row_stride, int64_t rows, int64_t vocab,
+                         const float* temperature, const int32_t* top_k, const float* top_p,
+                         uint64_t seed, int64_t* out, void* workspace, size_t workspace_bytes,
+                         void* stream);
 
 /* seq_lens[row_ids[i]] += delta for i < n, except rows equal to skip_row
  * (a captured batch's padding row) and rows outside [0, max_rows).  Rows

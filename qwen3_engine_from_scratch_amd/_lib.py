@@ -92,6 +92,9 @@ _SIGNATURES = {
     "qwen3_advance_seq_lens": (_i, [_vp, _i64, _vp, _i, _i, _i, _vp]),
     "qwen3_page_in_bf16": (_i, [_vp, _i64, _i64, _i64, _vp, _i, _vp, _vp, _i64, _i64, _vp]),
     "qwen3_sample_bf16": (_i, [_vp, _i64, _i64, _i64, _vp, _vp, _vp, ctypes.c_uint64, _vp, _vp]),
+    "qwen3_sample_workspace_bytes": (ctypes.c_size_t, [_i64, _i64]),
+    "qwen3_sample_ws_bf16": (_i, [_vp, _i64, _i64, _i64, _vp, _vp, _vp, ctypes.c_uint64, _vp, _vp,
+                                  ctypes.c_size_t, _vp]),
     "qwen3_lm_head_argmax_workspace_bytes": (ctypes.c_size_t, []),
     "qwen3_lm_head_argmax_bf16": (_i, [_vp, _i64, _vp, _i, _vp, ctypes.c_float, _vp, _i64, _i,
                                        _i, _i, _vp, ctypes.c_size_t, _vp, _vp]),

@@ -36,6 +36,28 @@
 // from the tie indices themselves.
 // Masses are summed as 64-bit fixed point (2^40 per unit), so every
 // histogram and the cut are independent of summation order.
+//
+// With a workspace (qwen3_sample_ws_bf16) and at most 128 rows, the row is
+// first cut into P parts (P = 2..8, so rows x P workgroups fill the CUs),
+// and each part's workgroup keeps its tokens at or above a key that k of
+// them reach (the k-th largest of its threads' own maxima; the k-th
+// largest token's high bin when k is above the thread count).  Every token
+// at or above the row's k-th largest key is then kept: a part holding one
+// below its own threshold holds k tokens above it, more than the row has.
+// One workgroup per row then runs passes A to E over the concatenated lists
+// instead of the row (or over the row when a list overflowed or top-k cuts
+// nothing).  The lists hold the whole top-k list and every tie at its
+// boundary, and no step depends on the order of the candidates, so the
+// draws are the single workgroup's.  Greedy rows take each part's first
+// maximum and then the first among the parts.
+//
+// The VALU is the limit of every pass (a wave64 instruction occupies its
+// SIMD four cycles), so the per-token work is kept small: whole rounds of
+// a thread's 8 tokens are tested without per-token bounds checks, a part's
+// first pass takes only per-thread maxima on packed 16-bit keys (two tokens
+// per instruction), and the list pass skips a round on its packed maximum.
+#include <type_traits>
+
 #include "common.hpp"
 
 namespace {
@@ -53,6 +75,53 @@ __device__ __forceinline__ uint32_t okey(uint32_t b) {
 __device__ __forceinline__ float key_value(uint32_t key) {
   const uint32_t b = (key & 0x8000u) ? (key & 0x7FFFu) : (~key & 0xFFFFu);
   return __uint_as_float(b << 16);
+}
+// The keys of a pair of bf16 (low and high half of x) without the NaN
+// test: a number's key, NaN above +inf (positive sign) or below -inf
+// (negative sign).  Two instructions for two tokens (a packed 16-bit
+// arithmetic shift gives each negative half its flip mask).
+typedef int16_t i16x2 __attribute__((ext_vector_type(2)));
+typedef uint16_t u16x2 __attribute__((ext_vector_type(2)));
+__device__ __forceinline__ uint32_t raw_keys2(uint32_t x) {
+  const i16x2 sign = __builtin_bit_cast(i16x2, x) >> static_cast<int16_t>(15);
+  return x ^ (__builtin_bit_cast(uint32_t, sign) | 0x80008000u);
+}
+__device__ __forceinline__ uint32_t max_u16x2(uint32_t a, uint32_t b) {
+  return __builtin_bit_cast(uint32_t, __builtin_elementwise_max(__builtin_bit_cast(u16x2, a),
+                                                                __builtin_bit_cast(u16x2, b)));
+}
+// The largest raw key of a whole round's 8 tokens (b as unpacked by the
+// visitor).  Equal to the largest key unless the round holds a NaN: then it
+// is above 0xFF80 (a positive NaN) or, with only negative NaNs above -inf's
+// key 0x7F, below 0x7F.
+__device__ __forceinline__ uint32_t round_raw_max(const uint32_t* b) {
+  uint32_t m = 0;
+#pragma unroll
+  for (int j = 0; j < 4; ++j) m = max_u16x2(m, raw_keys2(b[2 * j] | (b[2 * j + 1] << 16)));
+  return (m & 0xFFFFu) > (m >> 16) ? (m & 0xFFFFu) : (m >> 16);
+}
+
+// Greedy order: the same key with every NaN above every number (0xFFFF,
+// which no number maps to), as torch.argmax ranks them.
+__device__ __forceinline__ uint32_t gkey(uint32_t b) {
+  return (b & 0x7FFFu) > 0x7F80u ? 0xFFFFu : ((b & 0x8000u) ? (~b & 0xFFFFu) : (b | 0x8000u));
+}
+// One thread's greedy candidate among its 8 tokens i0 .. i0 + 7 of a round
+// (those below n when the round is partial): (gkey + 1) << 32 | ~index of
+// the first largest, 0 when none is valid.  The 8 are ranked on 19-bit
+// packed keys (gkey << 3 | 7 - e: the lower e wins a tie) without a branch.
+template <typename Full>
+__device__ __forceinline__ unsigned long long greedy_round(int64_t i0, const uint32_t* b,
+                                                          int64_t n, Full full) {
+  uint32_t m = 0;
+#pragma unroll
+  for (int e = 0; e < 8; ++e) {
+    const uint32_t pk = (gkey(b[e]) << 3) | (7u - e);
+    if (full || i0 + e < n) m = pk > m ? pk : m;
+  }
+  const uint32_t idx = static_cast<uint32_t>(i0) + (7u - (m & 7u));
+  const unsigned long long c = (static_cast<unsigned long long>((m >> 3) + 1) << 32) | ~idx;
+  return m ? c : 0ull;
 }
 
 // Philox4x32-10 (Salmon, Moraes, Dror, Shaw, "Parallel random numbers: as
@@ -112,6 +181,98 @@ struct Shared {
   int ncand, nties;
   uint32_t idx_cut;
 };
+
+// One part's results of the parallel passes (one per row and part, in the
+// workspace).
+struct alignas(16) PartOut {
+  uint32_t cnt[kHiBins];        // pass A: high-bin counts (sampled rows)
+  uint32_t lo_cnt[kLoBins];     // pass B: low-bin counts inside the boundary bin
+  uint32_t kmax;                // pass A: largest key
+  int32_t ncand;                // pass B: candidates written, -1 none
+  unsigned long long best;      // greedy rows: (key + 1) << 32 | ~index, the part's first maximum
+  unsigned long long cand[kCap];  // pass B: (key << 32) | token index
+};
+
+// Parts per row of the parallel form: about one workgroup per CU over the
+// batch (four parts for 64 rows measured best on 256 CUs: 44 us against
+// 55 for two and 65 for eight), each part at least one round (kThreads * 8
+// tokens); 1 means the single-workgroup form.
+constexpr int kMaxParts = 8;
+__host__ __device__ inline int parts_for(int64_t rows, int64_t vocab) {
+  int p = rows <= 32 ? kMaxParts : rows <= 64 ? 4 : rows <= 128 ? 2 : 1;
+  const int64_t rounds = (vocab + kThreads * 8 - 1) / (kThreads * 8);
+  return static_cast<int>(p < rounds ? p : rounds);
+}
+// Tokens [lo, hi) of part c: whole rounds, the last part takes the rest.
+__device__ __forceinline__ void part_range(int64_t vocab, int P, int c, int64_t& lo, int64_t& hi) {
+  const int64_t per = kThreads * 8;
+  const int64_t rounds = (vocab + per - 1) / per;
+  const int64_t rp = (rounds + P - 1) / P;
+  lo = c * rp * per;
+  hi = lo + rp * per < vocab ? lo + rp * per : vocab;
+  if (lo > vocab) lo = vocab;
+}
+
+// Block-wide maximum; every thread gets the result.
+__device__ __forceinline__ unsigned long long block_max_u64(unsigned long long v, Shared& sh) {
+#pragma unroll
+  for (int m = 1; m < 64; m <<= 1) {
+    const unsigned long long o = __shfl_xor(v, m, 64);
+    v = o > v ? o : v;
+  }
+  __syncthreads();
+  if ((threadIdx.x & 63) == 0) sh.best[threadIdx.x >> 6] = v;
+  __syncthreads();
+  v = 0;
+#pragma unroll
+  for (int w = 0; w < kWaves; ++w) v = sh.best[w] > v ? sh.best[w] : v;
+  return v;
+}
+
+// Appends (key, index) of the lanes where q holds to the block's candidate
+// list (sh.cand, sh.ncand; entries past kCap are counted, not stored): one
+// LDS atomic per wave.  Called by every lane of the wave.
+__device__ __forceinline__ void append_candidate(bool q, uint32_t key, int64_t idx, Shared& sh) {
+  const int lane = threadIdx.x & 63;
+  const unsigned long long m = __ballot(q);
+  if (m == 0ull) return;
+  const int leader = __ffsll(static_cast<long long>(m)) - 1;
+  int base = 0;
+  if (lane == leader) base = atomicAdd(&sh.ncand, __popcll(m));
+  base = __shfl(base, leader, 64);
+  if (q) {
+    const int pos = base + __popcll(m & ((1ull << lane) - 1ull));
+    if (pos < kCap)
+      sh.cand[pos] = (static_cast<unsigned long long>(key) << 32) | static_cast<uint32_t>(idx);
+  }
+}
+
+// The same for the tokens i0 + e of a thread's round where q[e] holds
+// (keys[e] their keys): a wave prefix sum places them, one LDS atomic per
+// wave.  Called by every lane of the wave.
+__device__ __forceinline__ void append_round(const bool (&q)[8], const uint32_t (&keys)[8],
+                                             int64_t i0, Shared& sh) {
+  const int lane = threadIdx.x & 63;
+  int c = 0;
+#pragma unroll
+  for (int e = 0; e < 8; ++e) c += q[e] ? 1 : 0;
+  int incl = c;
+#pragma unroll
+  for (int o = 1; o < 64; o <<= 1) {
+    const int y = __shfl_up(incl, o, 64);
+    if (lane >= o) incl += y;
+  }
+  int base = 0;
+  if (lane == 63) base = atomicAdd(&sh.ncand, incl);
+  int pos = __shfl(base, 63, 64) + incl - c;
+#pragma unroll
+  for (int e = 0; e < 8; ++e) {
+    if (!q[e]) continue;
+    if (pos < kCap)
+      sh.cand[pos] = (static_cast<unsigned long long>(keys[e]) << 32) | static_cast<uint32_t>(i0 + e);
+    ++pos;
+  }
+}
 
 // Block-wide sums; every thread gets the result.
 __device__ __forceinline__ int block_sum_int(int v, Shared& sh) {
@@ -174,42 +335,92 @@ __device__ __forceinline__ unsigned long long block_scan_u64(unsigned long long 
 }
 
 // Visits the row in rounds of kThreads * 8 tokens: thread t gets tokens
-// base + 8t .. base + 8t + 7 of each round (16-byte loads when aligned).  The
+// base + 8t .. base + 8t + 7 of each round (16-byte loads when aligned), as
+// f(i0, b, full) with `full` a compile-time true when the whole round lies
+// inside the row (no token needs a bounds test) and false for the row's
+// last, partial round.  The
 // loads of kBatch rounds are issued before any is used, so a pass over the
-// row waits for memory once per batch rather than once per round.
-template <bool kVec, typename F>
-__device__ __forceinline__ void for_each_round(const uint16_t* p, int64_t vocab, F&& f) {
-  constexpr int kBatch = kVec ? 8 : 2;  // element loads hold more registers
-  const int64_t per_round = static_cast<int64_t>(kThreads) * 8;
-  for (int64_t base = 0; base < vocab; base += per_round * kBatch) {
-    q3::u32x4 v[kBatch];
+// row waits for memory once per batch rather than once per round.  The
+// 16-byte loads sit in no branch (a lane whose 8 tokens pass the row's end
+// loads the row's first 8 instead and patches its tokens afterwards): a
+// load under a divergent branch makes the compiler wait for it at the
+// branch's end, one memory round trip per round.
+template <bool kVec>
+constexpr int batch_rounds() {
+  return kVec ? 8 : 2;  // element loads hold more registers
+}
+constexpr int64_t kPerRound = static_cast<int64_t>(kThreads) * 8;
+
+// Loads the rounds base .. base + kBatch - 1 of the row into v.
+template <bool kVec, int kBatch>
+__device__ __forceinline__ void load_rounds(const uint16_t* p, int64_t vocab, int64_t base,
+                                            q3::u32x4 (&v)[kBatch]) {
+  const int64_t lane0 = 8 * static_cast<int64_t>(threadIdx.x);
+  if (kVec && vocab >= 8) {
 #pragma unroll
     for (int u = 0; u < kBatch; ++u) {
-      const int64_t i0 = base + u * per_round + 8 * static_cast<int64_t>(threadIdx.x);
-      if (kVec && i0 + 8 <= vocab) {
-        v[u] = q3::ld16(p + i0);
-      } else {
-#pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          const uint32_t lo = i0 + 2 * e < vocab ? p[i0 + 2 * e] : 0x7FC1u;  // NaN pad
-          const uint32_t hi = i0 + 2 * e + 1 < vocab ? p[i0 + 2 * e + 1] : 0x7FC1u;
-          v[u][e] = lo | (hi << 16);
-        }
-      }
-    }
-#pragma unroll
-    for (int u = 0; u < kBatch; ++u) {
-      const int64_t i0 = base + u * per_round + 8 * static_cast<int64_t>(threadIdx.x);
-      if (base + u * per_round >= vocab) break;  // uniform: the round is past the row
-      uint32_t b[8];
-#pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        b[2 * e] = v[u][e] & 0xFFFFu;
-        b[2 * e + 1] = v[u][e] >> 16;
-      }
-      f(i0, b);
+      if (base + u * kPerRound >= vocab) break;  // uniform: the round is past the row
+      const int64_t i0 = base + u * kPerRound + lane0;
+      v[u] = q3::ld16(p + (i0 + 8 <= vocab ? i0 : 0));
     }
   }
+  if (!kVec || vocab < 8 || base + kPerRound * kBatch > vocab) {  // uniform: the row ends here
+#pragma unroll
+    for (int u = 0; u < kBatch; ++u) {
+      if (base + u * kPerRound >= vocab) break;
+      const int64_t i0 = base + u * kPerRound + lane0;
+      if (kVec && vocab >= 8 && i0 + 8 <= vocab) continue;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const uint32_t lo = i0 + 2 * e < vocab ? p[i0 + 2 * e] : 0x7FC1u;  // NaN pad
+        const uint32_t hi = i0 + 2 * e + 1 < vocab ? p[i0 + 2 * e + 1] : 0x7FC1u;
+        v[u][e] = lo | (hi << 16);
+      }
+    }
+  }
+}
+
+// Calls f(i0, b, full) for the loaded rounds that lie in the row.
+template <int kBatch, typename F>
+__device__ __forceinline__ void visit_rounds(int64_t vocab, int64_t base,
+                                             const q3::u32x4 (&v)[kBatch], F&& f) {
+  const int64_t lane0 = 8 * static_cast<int64_t>(threadIdx.x);
+#pragma unroll
+  for (int u = 0; u < kBatch; ++u) {
+    const int64_t i0 = base + u * kPerRound + lane0;
+    if (base + u * kPerRound >= vocab) break;  // uniform: the round is past the row
+    uint32_t b[8];
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      b[2 * e] = v[u][e] & 0xFFFFu;
+      b[2 * e + 1] = v[u][e] >> 16;
+    }
+    if (base + (u + 1) * kPerRound <= vocab)  // uniform
+      f(i0, b, std::true_type{});
+    else
+      f(i0, b, std::false_type{});
+  }
+}
+
+template <bool kVec, typename F>
+__device__ __forceinline__ void for_each_round(const uint16_t* p, int64_t vocab, F&& f) {
+  constexpr int kBatch = batch_rounds<kVec>();
+  for (int64_t base = 0; base < vocab; base += kPerRound * kBatch) {
+    q3::u32x4 v[kBatch];
+    load_rounds<kVec, kBatch>(p, vocab, base, v);
+    visit_rounds<kBatch>(vocab, base, v, f);
+  }
+}
+
+// The same over tokens [lo, hi) of the row (lo a multiple of 8): f gets the
+// row index of the first of its 8 tokens.
+template <bool kVec, typename F>
+__device__ __forceinline__ void for_each_round_in(const uint16_t* p, int64_t lo, int64_t hi,
+                                                  F&& f) {
+  if (hi <= lo) return;
+  for_each_round<kVec>(p + lo, hi - lo, [&](int64_t i0, const uint32_t* b, auto full) {
+    f(lo + i0, b, full);
+  });
 }
 
 // Scans the low-bit count histogram from the top: returns the bin where the
@@ -291,34 +502,200 @@ __device__ __forceinline__ int find_mass_bin_block(const unsigned long long* m, 
   return sh.sel_bin;
 }
 
+// A value of each of a row's P parts, all loads issued before any is used
+// (a loop over a runtime part count would wait for each in turn); parts
+// past P read part 0 and count as `none`.
+template <typename T, typename F>
+__device__ __forceinline__ void part_values(int P, T none, F&& get, T (&v)[kMaxParts]) {
+  T raw[kMaxParts];
+#pragma unroll
+  for (int c = 0; c < kMaxParts; ++c) raw[c] = get(c < P ? c : 0);
+#pragma unroll
+  for (int c = 0; c < kMaxParts; ++c) v[c] = c < P ? raw[c] : none;
+}
+
+// The parallel form's first kernel, workgroup (row, part): for a greedy row
+// the part's first maximum; for a row that top-k cuts, the part's largest
+// key and its tokens at or above its own threshold (a list of -1 entries:
+// more than kCap, or nothing cut by top-k).  A part of at most 8 rounds is
+// held in registers for both of its passes.
 template <bool kVec>
+__global__ __launch_bounds__(kThreads) void sample_part_kernel(const uint16_t* logits,
+                                                               int64_t row_s, int64_t vocab,
+                                                               const float* temperature,
+                                                               const int32_t* top_k, int P,
+                                                               PartOut* parts) {
+  __shared__ Shared sh;
+  const int64_t row = blockIdx.x / P;
+  const int c = static_cast<int>(blockIdx.x % P);
+  const uint16_t* p = logits + row * row_s;
+  const bool greedy = !((temperature ? temperature[row] : 0.f) > 0.f);
+  const int64_t kreq = top_k ? top_k[row] : 0;
+  const int tid = threadIdx.x;
+  int64_t lo, hi;
+  part_range(vocab, P, c, lo, hi);
+  PartOut& po = parts[row * P + c];
+  if (!greedy && (kreq <= 0 || kreq >= vocab)) {  // top-k cuts nothing: no list
+    if (tid == 0) po.ncand = -1;
+    return;
+  }
+  if (!greedy) {
+    for (int i = tid; i < kHiBins; i += kThreads) sh.cnt[i] = 0;
+    if (tid == 0) sh.ncand = 0;
+    __syncthreads();
+  }
+  if (greedy) {  // the part's first largest value, as the single-workgroup greedy path
+    unsigned long long best = 0;
+    for_each_round_in<kVec>(p, lo, hi, [&](int64_t i0, const uint32_t* b, auto full) {
+      const unsigned long long cb = greedy_round(i0, b, hi, full);
+      best = cb > best ? cb : best;
+    });
+    best = block_max_u64(best, sh);
+    if (tid == 0) po.best = best;
+    return;
+  }
+  // The part keeps every token whose key is >= t_lo, a key that at least
+  // kreq of the part's tokens reach: then a part token below t_lo has kreq
+  // tokens of the row strictly above it, so the list holds every token at
+  // or above the row's k-th largest key.  t_lo is the kreq-th largest of the
+  // threads' own largest keys (kreq threads reaching it are kreq distinct
+  // tokens), found on a histogram of those, one LDS atomic per thread; a
+  // kreq above the thread count takes the high bin of the kreq-th largest
+  // token from a histogram of every token instead.
+  const int64_t n_part = hi - lo;
+  auto passes = [&](auto&& visit) {
+    // each thread's largest key: whole rounds on raw keys, a NaN seen there
+    // sends the thread through its tokens again on exact keys
+    uint32_t tmax = 0, rmax = 0;
+    visit([&](int64_t i0, const uint32_t* b, auto full) {
+      if constexpr (decltype(full)::value) {
+        const uint32_t m = round_raw_max(b);
+        rmax = m > rmax ? m : rmax;
+      } else {
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          const uint32_t key = okey(b[e]);
+          if (i0 + e < hi) tmax = key > tmax ? key : tmax;
+        }
+      }
+    });
+    if (rmax > 0xFF80u) {  // a positive NaN in a whole round: exact keys
+      tmax = 0;
+      visit([&](int64_t i0, const uint32_t* b, auto full) {
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          const uint32_t key = okey(b[e]);
+          if (full || i0 + e < hi) tmax = key > tmax ? key : tmax;
+        }
+      });
+    } else if (rmax >= 0x7Fu) {  // else no whole round, or only negative NaNs (key 0)
+      tmax = rmax > tmax ? rmax : tmax;
+    }
+    const bool has = 8 * static_cast<int64_t>(tid) < n_part;  // the thread holds tokens
+    if (has) atomicAdd(&sh.cnt[tmax >> kLoBits], 1u);
+    if (tid < kLoBins) sh.lo_cnt[tid] = 0;
+    const uint32_t kmax = static_cast<uint32_t>(block_max_u64(tmax, sh));  // syncs the counts
+    const int64_t n_thr = n_part < 8 * kThreads ? (n_part + 7) / 8 : kThreads;
+    uint32_t t_lo = 0;  // keys kept: >= t_lo (a part of at most kreq tokens keeps them all)
+    if (n_part > kreq && kreq <= n_thr) {
+      // the kreq-th largest thread maximum: its high bin, then its low bits
+      int64_t above = 0;
+      const int hb = find_count_bin_block(sh.cnt, kreq, above, sh);
+      if (has && static_cast<int>(tmax >> kLoBits) == hb)
+        atomicAdd(&sh.lo_cnt[tmax & (kLoBins - 1)], 1u);
+      __syncthreads();
+      const int lb = find_count_bin(sh.lo_cnt, kreq, above);
+      t_lo = (static_cast<uint32_t>(hb) << kLoBits) | static_cast<uint32_t>(lb);
+    } else if (n_part > kreq) {
+      for (int i = tid; i < kHiBins; i += kThreads) sh.cnt[i] = 0;
+      __syncthreads();
+      visit([&](int64_t i0, const uint32_t* b, auto full) {
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          if (!full && i0 + e >= hi) break;
+          atomicAdd(&sh.cnt[okey(b[e]) >> kLoBits], 1u);
+        }
+      });
+      __syncthreads();
+      int64_t above = 0;
+      t_lo = static_cast<uint32_t>(find_count_bin_block(sh.cnt, kreq, above, sh)) << kLoBits;
+    }
+    visit([&](int64_t i0, const uint32_t* b, auto full) {
+      // most rounds keep nothing of the wave: a whole round is passed over
+      // on its raw maximum (a NaN there only sends it to the exact test)
+      if constexpr (decltype(full)::value)
+        if (__ballot(round_raw_max(b) >= t_lo) == 0ull) return;
+      bool q[8], any = false;
+      uint32_t keys[8];
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        keys[e] = okey(b[e]);
+        q[e] = (full || i0 + e < hi) && keys[e] >= t_lo;
+        any = any || q[e];
+      }
+      if (__ballot(any) == 0ull) return;
+      append_round(q, keys, i0, sh);
+    });
+    __syncthreads();
+    const int n = sh.ncand;
+    const bool ok = n <= kCap;
+    if (tid == 0) {
+      po.kmax = kmax;
+      po.ncand = ok ? n : -1;
+    }
+    if (ok)
+      for (int i = tid; i < n; i += kThreads) po.cand[i] = sh.cand[i];
+  };
+  constexpr int kB = batch_rounds<kVec>();
+  if (n_part <= kB * kPerRound) {  // one batch: both passes over registers
+    q3::u32x4 v[kB];
+    load_rounds<kVec, kB>(p + lo, n_part, 0, v);
+    passes([&](auto&& f) {
+      visit_rounds<kB>(n_part, 0, v, [&](int64_t i0, const uint32_t* b, auto full) {
+        f(lo + i0, b, full);
+      });
+    });
+  } else {
+    passes([&](auto&& f) { for_each_round_in<kVec>(p, lo, hi, f); });
+  }
+}
+
+// One workgroup per row.  kPre: greedy rows and, when every part kept its
+// list, passes A and B run over the parts' lists instead of the row;
+// otherwise the workgroup streams the row for them itself.
+template <bool kVec, bool kPre>
 __global__ __launch_bounds__(kThreads) void sample_kernel(const uint16_t* logits, int64_t row_s,
                                                           int64_t vocab, const float* temperature,
                                                           const int32_t* top_k,
                                                           const float* top_p, uint64_t seed,
-                                                          int64_t* out) {
+                                                          int64_t* out, int P,
+                                                          const PartOut* parts) {
   __shared__ Shared sh;
   const int64_t row = blockIdx.x;
   const uint16_t* p = logits + row * row_s;
   const float temp = temperature ? temperature[row] : 0.f;
   const int tid = threadIdx.x;
   const int lane = tid & 63, wave = tid >> 6;
+  const PartOut* rp = kPre ? parts + row * P : nullptr;
 
   // ---- greedy -----------------------------------------------------------
+  if (kPre && !(temp > 0.f)) {
+    if (tid == 0) {
+      unsigned long long v[kMaxParts];
+      part_values(P, 0ull, [&](int c) { return rp[c].best; }, v);
+      unsigned long long b = 0;
+#pragma unroll
+      for (int c = 0; c < kMaxParts; ++c) b = v[c] > b ? v[c] : b;
+      out[row] = static_cast<int64_t>(~static_cast<uint32_t>(b));
+    }
+    return;
+  }
   if (!(temp > 0.f)) {
     // first index of the largest value; NaN ranks highest, as torch.argmax
     unsigned long long bestk = 0;
-    for_each_round<kVec>(p, vocab, [&](int64_t i0, const uint32_t* b) {
-#pragma unroll
-      for (int e = 0; e < 8; ++e) {
-        if (i0 + e >= vocab) break;
-        const uint32_t bb = b[e];
-        const bool nan = (bb & 0x7F80u) == 0x7F80u && (bb & 0x7Fu);
-        const uint32_t k = nan ? 0x10000u : okey(bb);
-        const unsigned long long key =
-            (static_cast<unsigned long long>(k + 1) << 32) | (~static_cast<uint32_t>(i0 + e));
-        bestk = key > bestk ? key : bestk;
-      }
+    for_each_round<kVec>(p, vocab, [&](int64_t i0, const uint32_t* b, auto full) {
+      const unsigned long long cb = greedy_round(i0, b, vocab, full);
+      bestk = cb > bestk ? cb : bestk;
     });
 #pragma unroll
     for (int m = 1; m < 64; m <<= 1) {
@@ -343,19 +720,7 @@ __global__ __launch_bounds__(kThreads) void sample_kernel(const uint16_t* logits
 
   // Appends (key, index) of the lanes where q holds to the candidate list:
   // one LDS atomic per wave.  Called by every lane of the wave.
-  auto compact = [&](bool q, uint32_t key, int64_t idx) {
-    const unsigned long long m = __ballot(q);
-    if (m == 0ull) return;
-    const int leader = __ffsll(static_cast<long long>(m)) - 1;
-    int base = 0;
-    if (lane == leader) base = atomicAdd(&sh.ncand, __popcll(m));
-    base = __shfl(base, leader, 64);
-    if (q) {
-      const int pos = base + __popcll(m & ((1ull << lane) - 1ull));
-      if (pos < kCap)
-        sh.cand[pos] = (static_cast<unsigned long long>(key) << 32) | static_cast<uint32_t>(idx);
-    }
-  };
+  auto compact = [&](bool q, uint32_t key, int64_t idx) { append_candidate(q, key, idx, sh); };
   // Once the candidate list holds every token that can still be kept
   // (ncand >= 0), the later passes visit it instead of the row.
   int ncand = -1;
@@ -366,10 +731,10 @@ __global__ __launch_bounds__(kThreads) void sample_kernel(const uint16_t* logits
         f(static_cast<uint32_t>(c >> 32), static_cast<int64_t>(static_cast<uint32_t>(c)));
       }
     } else {
-      for_each_round<kVec>(p, vocab, [&](int64_t i0, const uint32_t* b) {
+      for_each_round<kVec>(p, vocab, [&](int64_t i0, const uint32_t* b, auto full) {
 #pragma unroll
         for (int e = 0; e < 8; ++e)
-          if (i0 + e < vocab) f(okey(b[e]), i0 + e);
+          if (full || i0 + e < vocab) f(okey(b[e]), i0 + e);
       });
     }
   };
@@ -389,30 +754,73 @@ __global__ __launch_bounds__(kThreads) void sample_kernel(const uint16_t* logits
   };
 
   // ---- A: high-bin counts and the maximum key ----------------------------
-  for (int i = tid; i < kHiBins; i += kThreads) sh.cnt[i] = 0;
-  if (tid < kLoBins) sh.lo_cnt[tid] = 0;
-  if (tid == 0) sh.ncand = 0;
-  __syncthreads();
   uint32_t kmax = 0;
-  for_each_round<kVec>(p, vocab, [&](int64_t i0, const uint32_t* b) {
+  bool from_list = false;  // the parts' lists stand for the row in passes A, B
+  if constexpr (kPre) {
+    int nc[kMaxParts];
+    part_values(P, 0, [&](int c) { return rp[c].ncand; }, nc);
+    uint32_t km[kMaxParts];
+    part_values(P, 0u, [&](int c) { return rp[c].kmax; }, km);
+    int total = 0;
+    from_list = true;
 #pragma unroll
-    for (int e = 0; e < 8; ++e) {
-      if (i0 + e >= vocab) break;
-      const uint32_t key = okey(b[e]);
-      kmax = key > kmax ? key : kmax;
-      atomicAdd(&sh.cnt[key >> kLoBits], 1u);
+    for (int c = 0; c < kMaxParts; ++c) {
+      from_list = from_list && nc[c] >= 0;
+      total += nc[c] > 0 ? nc[c] : 0;
+      kmax = km[c] > kmax ? km[c] : kmax;
     }
-  });
+    from_list = from_list && total <= kCap;
+    if (from_list) {
+      for (int i = tid; i < kHiBins; i += kThreads) sh.cnt[i] = 0;
+      if (tid < kLoBins) sh.lo_cnt[tid] = 0;
+      __syncthreads();
+      // entry e of the concatenated lists: part c's run starts at the sum
+      // of the runs before it
+      for (int e = tid; e < total; e += kThreads) {
+        int c = 0, before = 0, start = 0;  // the last part whose run starts at or before e
 #pragma unroll
-  for (int m = 1; m < 64; m <<= 1) {
-    const uint32_t o = __shfl_xor(kmax, m, 64);
-    kmax = o > kmax ? o : kmax;
+        for (int j = 0; j < kMaxParts; ++j) {
+          if (e >= start) {
+            c = j;
+            before = start;
+          }
+          start += nc[j];
+        }
+        const unsigned long long cd = rp[c].cand[e - before];
+        sh.cand[e] = cd;
+        atomicAdd(&sh.cnt[static_cast<uint32_t>(cd >> 32) >> kLoBits], 1u);
+      }
+      ncand = total;
+      __syncthreads();
+    } else {
+      kmax = 0;
+    }
   }
-  if (lane == 0) sh.wmax[wave] = kmax;
-  __syncthreads();
-  kmax = 0;
+  if (!from_list) {
+    for (int i = tid; i < kHiBins; i += kThreads) sh.cnt[i] = 0;
+    if (tid < kLoBins) sh.lo_cnt[tid] = 0;
+    if (tid == 0) sh.ncand = 0;
+    __syncthreads();
+    for_each_round<kVec>(p, vocab, [&](int64_t i0, const uint32_t* b, auto full) {
 #pragma unroll
-  for (int w = 0; w < kWaves; ++w) kmax = sh.wmax[w] > kmax ? sh.wmax[w] : kmax;
+      for (int e = 0; e < 8; ++e) {
+        if (!full && i0 + e >= vocab) break;
+        const uint32_t key = okey(b[e]);
+        kmax = key > kmax ? key : kmax;
+        atomicAdd(&sh.cnt[key >> kLoBits], 1u);
+      }
+    });
+#pragma unroll
+    for (int m = 1; m < 64; m <<= 1) {
+      const uint32_t o = __shfl_xor(kmax, m, 64);
+      kmax = o > kmax ? o : kmax;
+    }
+    if (lane == 0) sh.wmax[wave] = kmax;
+    __syncthreads();
+    kmax = 0;
+#pragma unroll
+    for (int w = 0; w < kWaves; ++w) kmax = sh.wmax[w] > kmax ? sh.wmax[w] : kmax;
+  }
   const float xmax = key_value(kmax) * inv_t;
 
   // ---- B: exact k-th largest key (kk) and the ties of it kept (tk) ------
@@ -423,17 +831,32 @@ __global__ __launch_bounds__(kThreads) void sample_kernel(const uint16_t* logits
     const int hb = find_count_bin_block(sh.cnt, k, above, sh);
     // the tokens of bins >= hb hold the top-k list: keep them when they fit
     const bool keep_list = above + static_cast<int64_t>(sh.cnt[hb]) <= kCap;
-    for_each_round<kVec>(p, vocab, [&](int64_t i0, const uint32_t* b) {
-#pragma unroll
-      for (int e = 0; e < 8; ++e) {
-        const bool valid = i0 + e < vocab;
-        const uint32_t key = okey(b[e]);
-        const int kb = static_cast<int>(key >> kLoBits);
-        if (valid && kb == hb) atomicAdd(&sh.lo_cnt[key & (kLoBins - 1)], 1u);
-        if (keep_list) compact(valid && kb >= hb, key, i0 + e);
+    if (from_list) {
+      // the low-bin counts inside bin hb, over the list (which holds every
+      // token at or above the k-th largest key: those counts are the row's)
+      for (int i = tid; i < ncand; i += kThreads) {
+        const uint32_t key = static_cast<uint32_t>(sh.cand[i] >> 32);
+        if (static_cast<int>(key >> kLoBits) == hb) atomicAdd(&sh.lo_cnt[key & (kLoBins - 1)], 1u);
       }
-    });
-    if (keep_list) finish_compaction();
+    } else {
+      for_each_round<kVec>(p, vocab, [&](int64_t i0, const uint32_t* b, auto full) {
+        bool q[8], any = false;  // tokens at or above the boundary bin
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          q[e] = (full || i0 + e < vocab) && static_cast<int>(okey(b[e]) >> kLoBits) >= hb;
+          any = any || q[e];
+        }
+        if (__ballot(any) == 0ull) return;  // most rounds: none in the wave
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          const uint32_t key = okey(b[e]);
+          if (q[e] && static_cast<int>(key >> kLoBits) == hb)
+            atomicAdd(&sh.lo_cnt[key & (kLoBins - 1)], 1u);
+          if (keep_list) compact(q[e], key, i0 + e);
+        }
+      });
+      if (keep_list) finish_compaction();
+    }
     __syncthreads();
     const int lb = find_count_bin(sh.lo_cnt, k, above);
     kk = (static_cast<uint32_t>(hb) << kLoBits) | static_cast<uint32_t>(lb);
@@ -489,14 +912,21 @@ __global__ __launch_bounds__(kThreads) void sample_kernel(const uint16_t* logits
       } else {
         // the tokens that can be kept lie in bins >= hb: keep them when they fit
         const bool keep_list = count_from(hb) <= kCap;
-        for_each_round<kVec>(p, vocab, [&](int64_t i0, const uint32_t* b) {
+        for_each_round<kVec>(p, vocab, [&](int64_t i0, const uint32_t* b, auto full) {
+          bool q[8], any = false;  // tokens that can still be kept
 #pragma unroll
           for (int e = 0; e < 8; ++e) {
-            const bool valid = i0 + e < vocab;
             const uint32_t key = okey(b[e]);
-            if (valid) lo_hist(key, i0 + e);
-            if (keep_list)
-              compact(valid && static_cast<int>(key >> kLoBits) >= hb && key >= kk, key, i0 + e);
+            q[e] = (full || i0 + e < vocab) && static_cast<int>(key >> kLoBits) >= hb &&
+                   key >= kk;
+            any = any || q[e];
+          }
+          if (__ballot(any) == 0ull) return;  // most rounds: none in the wave
+#pragma unroll
+          for (int e = 0; e < 8; ++e) {
+            const uint32_t key = okey(b[e]);
+            if (q[e]) lo_hist(key, i0 + e);
+            if (keep_list) compact(q[e], key, i0 + e);
           }
         });
         if (keep_list) finish_compaction();
@@ -592,7 +1022,7 @@ __global__ __launch_bounds__(kThreads) void sample_kernel(const uint16_t* logits
     }
   } else {
     int64_t ties_before = 0;
-    for_each_round<kVec>(p, vocab, [&](int64_t i0, const uint32_t* b) {
+    for_each_round<kVec>(p, vocab, [&](int64_t i0, const uint32_t* b, auto) {
       int rank0 = 0;
       if (need_rank) {
         int c = 0;
@@ -655,10 +1085,68 @@ extern "C" int qwen3_sample_bf16(const void* logits, int64_t row_stride, int64_t
   auto s = static_cast<hipStream_t>(stream);
   const auto lg = static_cast<const uint16_t*>(logits);
   if (q3::aligned16(logits) && row_stride % 8 == 0)
-    hipLaunchKernelGGL(sample_kernel<true>, dim3(static_cast<unsigned>(rows)), dim3(kThreads), 0,
-                       s, lg, row_stride, vocab, temperature, top_k, top_p, seed, out);
+    hipLaunchKernelGGL((sample_kernel<true, false>), dim3(static_cast<unsigned>(rows)),
+                       dim3(kThreads), 0, s, lg, row_stride, vocab, temperature, top_k, top_p,
+                       seed, out, 0, nullptr);
   else
-    hipLaunchKernelGGL(sample_kernel<false>, dim3(static_cast<unsigned>(rows)), dim3(kThreads), 0,
-                       s, lg, row_stride, vocab, temperature, top_k, top_p, seed, out);
+    hipLaunchKernelGGL((sample_kernel<false, false>), dim3(static_cast<unsigned>(rows)),
+                       dim3(kThreads), 0, s, lg, row_stride, vocab, temperature, top_k, top_p,
+                       seed, out, 0, nullptr);
+  return q3::launch_status(who);
+}
+
+extern "C" size_t qwen3_sample_workspace_bytes(int64_t rows, int64_t vocab) {
+  if (rows <= 0 || vocab <= 0) return 0;
+  const int P = parts_for(rows, vocab);
+  return P > 1 ? static_cast<size_t>(rows) * P * sizeof(PartOut) : 0;
+}
+
+namespace {
+template <bool kVec>
+void launch_parts(const uint16_t* lg, int64_t row_stride, int64_t rows, int64_t vocab,
+                  const float* temperature, const int32_t* top_k, const float* top_p,
+                  uint64_t seed, int64_t* out, int P, PartOut* parts, hipStream_t s) {
+  hipLaunchKernelGGL(sample_part_kernel<kVec>, dim3(static_cast<unsigned>(rows * P)),
+                     dim3(kThreads), 0, s, lg, row_stride, vocab, temperature, top_k, P, parts);
+  hipLaunchKernelGGL((sample_kernel<kVec, true>), dim3(static_cast<unsigned>(rows)),
+                     dim3(kThreads), 0, s, lg, row_stride, vocab, temperature, top_k, top_p, seed,
+                     out, P, parts);
+}
+}  // namespace
+
+extern "C" int qwen3_sample_ws_bf16(const void* logits, int64_t row_stride, int64_t rows,
+                                    int64_t vocab, const float* temperature,
+                                    const int32_t* top_k, const float* top_p, uint64_t seed,
+                                    int64_t* out, void* workspace, size_t workspace_bytes,
+                                    void* stream) {
+  const char* who = "qwen3_sample_ws_bf16";
+  // no workspace, or a batch that fills the CUs with one workgroup per row:
+  // the single-workgroup form
+  if (!workspace || parts_for(rows, vocab) <= 1)
+    return qwen3_sample_bf16(logits, row_stride, rows, vocab, temperature, top_k, top_p, seed,
+                             out, stream);
+  if (!logits || !out) return q3::fail(QWEN3_EINVAL, "%s: null pointer argument", who);
+  if (rows < 0 || rows > 0x7fffffff || vocab <= 0 || vocab > 0x7fffffff || row_stride < vocab)
+    return q3::fail(QWEN3_EINVAL, "%s: bad sizes", who);
+  if (rows == 0) return QWEN3_OK;
+  const int P = parts_for(rows, vocab);
+  if (static_cast<int64_t>(rows) * P > 0x7fffffff)
+    return q3::fail(QWEN3_EINVAL, "%s: bad sizes", who);
+  const size_t need = qwen3_sample_workspace_bytes(rows, vocab);
+  if (workspace_bytes < need)
+    return q3::fail(QWEN3_EINVAL, "%s: workspace of %zu bytes, %zu needed", who,
+                    workspace_bytes, need);
+  if (!q3::aligned16(workspace))
+    return q3::fail(QWEN3_EALIGN, "%s: workspace must be 16-byte aligned", who);
+  q3::clear_error();
+  auto s = static_cast<hipStream_t>(stream);
+  const auto lg = static_cast<const uint16_t*>(logits);
+  auto parts = static_cast<PartOut*>(workspace);
+  if (q3::aligned16(logits) && row_stride % 8 == 0)
+    launch_parts<true>(lg, row_stride, rows, vocab, temperature, top_k, top_p, seed, out, P,
+                       parts, s);
+  else
+    launch_parts<false>(lg, row_stride, rows, vocab, temperature, top_k, top_p, seed, out, P,
+                        parts, s);
   return q3::launch_status(who);
 }

@@ -5,12 +5,14 @@ temperature / top_k / top_p as scalars or per-row lists / tensors, returns
 (B, 1) int64.  Rows with temperature <= 0 take the argmax; the rest draw from
 softmax(logits / temperature) restricted to the top_k largest logits (all
 when top_k <= 0) and, within them, to the leading tokens whose mass before
-them is <= top_p.  Every row goes through one HIP launch (qwen3_sample_bf16),
-or the argmax kernel when all rows are greedy; there is no host round trip
-for per-row parameters given as device tensors.  The random stream is the
-kernel's own (Philox4x32-10), so draws match the reference in distribution,
-not token for token — as the reference's own Triton path does against its
-torch path (qwen3/sampling.py:17-20).
+them is <= top_p.  The rows go through the sampling kernels
+(qwen3_sample_ws_bf16: for batches of up to 128 rows two launches that
+split each row over 2-8 workgroups, else one workgroup per row), or, when
+all rows are greedy and the batch is larger, the argmax kernel; there is no
+host round trip for per-row parameters given as device tensors.  The random
+stream is the kernel's own (Philox4x32-10), so draws match the reference in
+distribution, not token for token — as the reference's own Triton path does
+against its torch path (qwen3/sampling.py:17-20).
 """
 from __future__ import annotations
 
@@ -51,6 +53,27 @@ def _all_greedy(temperature) -> bool:
     return float(temperature) <= 0
 
 
+_WORKSPACES: dict = {}
+
+
+def _workspace(dev, stream: int, B: int, V: int):
+    """The parallel form's workspace for this device and stream (grown, never
+    shrunk); None under graph capture when it would have to grow (the call
+    then takes the single-workgroup form, which needs none)."""
+    need = int(_lib.load().qwen3_sample_workspace_bytes(B, V))
+    if need == 0:  # one part per row: the single-workgroup form
+        return None
+    key = (str(dev), stream)
+    ws = _WORKSPACES.get(key)
+    if ws is not None and ws.numel() >= need:
+        return ws
+    if torch.cuda.is_current_stream_capturing():
+        return None
+    ws = torch.empty(need, dtype=torch.uint8, device=dev)
+    _WORKSPACES[key] = ws
+    return ws
+
+
 def sample_tokens(logits: torch.Tensor, temperature=0.0, top_k=0, top_p=1.0,
                   seed: int | None = None) -> torch.Tensor:
     """(B, V) bf16 logits -> (B, 1) int64 tokens (reference:
@@ -60,16 +83,28 @@ def sample_tokens(logits: torch.Tensor, temperature=0.0, top_k=0, top_p=1.0,
     assert logits.dtype == torch.bfloat16 and logits.stride(1) == 1
     B, V = logits.shape
     dev = _lib.require_hip(logits)
+    stream = _lib.stream_of(dev)
     if _all_greedy(temperature):
-        return argmax(logits).view(B, 1)
+        ws = _workspace(dev, stream, B, V)
+        if ws is None:  # one workgroup per row: the argmax kernel
+            return argmax(logits).view(B, 1)
+        # a small batch: the parallel form's greedy path (no temperatures:
+        # every row greedy), each row split over several workgroups
+        out = torch.empty(B, dtype=torch.int64, device=dev)
+        _lib.check(_lib.load().qwen3_sample_ws_bf16(
+            logits.data_ptr(), logits.stride(0), B, V, None, None, None, 0, out.data_ptr(),
+            ws.data_ptr(), ws.numel(), stream), "qwen3_sample_ws_bf16")
+        return out.view(B, 1)
     t = _param(temperature, B, dev, torch.float32)
     k = _param(top_k, B, dev, torch.int32)
     p = _param(top_p, B, dev, torch.float32)
     if seed is None:
         seed = _next_seed()
     out = torch.empty(B, dtype=torch.int64, device=dev)
-    rc = _lib.load().qwen3_sample_bf16(logits.data_ptr(), logits.stride(0), B, V, t.data_ptr(),
-                                       k.data_ptr(), p.data_ptr(), int(seed) & (2 ** 64 - 1),
-                                       out.data_ptr(), _lib.stream_of(dev))
-    _lib.check(rc, "qwen3_sample_bf16")
+    ws = _workspace(dev, stream, B, V)
+    rc = _lib.load().qwen3_sample_ws_bf16(
+        logits.data_ptr(), logits.stride(0), B, V, t.data_ptr(), k.data_ptr(), p.data_ptr(),
+        int(seed) & (2 ** 64 - 1), out.data_ptr(), None if ws is None else ws.data_ptr(),
+        0 if ws is None else ws.numel(), stream)
+    _lib.check(rc, "qwen3_sample_ws_bf16")
     return out.view(B, 1)

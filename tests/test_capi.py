@@ -166,6 +166,21 @@ def test_model_ops_reject_bad_arguments():
     assert lib.qwen3_sample_bf16(FAKE, 100, 4, 151936, None, None, None, 1, FAKE, None) == -1
     assert lib.qwen3_sample_bf16(None, 151936, 4, 151936, None, None, None, 1, FAKE, None) == -1
     assert lib.qwen3_sample_bf16(FAKE, 151936, 0, 151936, None, None, None, 1, FAKE, None) == 0
+    need = int(lib.qwen3_sample_workspace_bytes(64, 151936))
+    assert need == 64 * 4 * 49232          # 4 parts per row, one record per part
+    assert int(lib.qwen3_sample_workspace_bytes(16, 151936)) == 16 * 8 * 49232
+    assert int(lib.qwen3_sample_workspace_bytes(128, 151936)) == 128 * 2 * 49232
+    assert int(lib.qwen3_sample_workspace_bytes(600, 151936)) == 0  # one workgroup per row
+    assert int(lib.qwen3_sample_workspace_bytes(1, 1000)) == 0      # one round: one part
+    assert int(lib.qwen3_sample_workspace_bytes(1, 20000)) == 1 * 3 * 49232  # three rounds
+    assert lib.qwen3_sample_ws_bf16(FAKE, 151936, 64, 151936, None, None, None, 1, FAKE,
+                                    FAKE, need - 16, None) == -1  # workspace too small
+    assert lib.qwen3_sample_ws_bf16(FAKE, 151936, 64, 151936, None, None, None, 1, FAKE,
+                                    FAKE + 8, need, None) == -2   # misaligned workspace
+    assert lib.qwen3_sample_ws_bf16(FAKE, 100, 4, 151936, None, None, None, 1, FAKE,
+                                    FAKE, need, None) == -1       # stride < vocab
+    assert lib.qwen3_sample_ws_bf16(FAKE, 151936, 0, 151936, None, None, None, 1, FAKE,
+                                    FAKE, need, None) == 0
     assert lib.qwen3_page_in_bf16(FAKE, 8, 4, 16, FAKE, 2, FAKE, FAKE, 100, 10, None) == -1  # stride < pages
     assert lib.qwen3_page_in_bf16(FAKE, 16, 4, 16, FAKE, 2, FAKE, FAKE, 100, 10, None) == -2  # odd block
     s2, s4 = _s(2048, 128), _s(1 << 16, 1 << 14, 2048, 128)

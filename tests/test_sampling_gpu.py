@@ -1,4 +1,5 @@
-"""GPU token sampling (qwen3_sample_bf16) against the sampling oracle.
+"""GPU token sampling (qwen3_sample_bf16, qwen3_sample_ws_bf16) against the
+sampling oracle, and the parallel form against the single-workgroup form.
 
 Bars: greedy rows equal torch.argmax exactly; every sampled token lies in
 the oracle's kept set; over many independent draws the empirical frequency
@@ -31,8 +32,30 @@ def test_greedy_rows_equal_argmax(gpu):
     for r in range(8):
         if t[r] <= 0:
             assert out[r] == ref[r], r
-    # all greedy: the argmax kernel
+    # all greedy: the parallel form's greedy path (8 rows: eight parts each)
     assert torch.equal(sample_tokens(x.to(gpu)).cpu().view(-1), ref)
+
+
+@pytest.mark.parametrize("B", [1, 33, 64, 128, 129, 300])
+def test_all_greedy_batches_equal_argmax(gpu, B):
+    """All-greedy batches: up to 128 rows through the parallel form's
+    greedy path (8, 4 or 2 parts per row), above that the argmax kernel;
+    ties keep the first index, NaN ranks above every number, a row of -inf
+    gives index 0."""
+    from qwen3_engine_from_scratch_amd.sampling import sample_tokens
+
+    announce(f"sampling: all greedy B={B}")
+    x = _logits(B, 151936, 7 + B)
+    x[0, 151935] = 60.0                          # maximum in the last token
+    if B > 1:
+        x[B - 1, 9000] = x[B - 1, 140000] = 55.0  # tie across parts: first index
+    if B > 3:
+        x[2, 100] = x[2, 30000] = float("nan")    # NaN ranks highest, first NaN
+        x[3] = float("-inf")
+    ref = torch.argmax(x, -1)
+    assert ref[0] == 151935
+    out = sample_tokens(x.to(gpu)).cpu().view(-1)
+    assert torch.equal(out, ref), (out != ref).nonzero().view(-1)[:8].tolist()
 
 
 @pytest.mark.parametrize("V,top_k,top_p,temp", [(151936, 50, 0.9, 1.0), (151936, 0, 0.8, 0.7),
@@ -126,3 +149,63 @@ def test_boundary_ties_keep_the_lower_index_and_seed_reproduces(gpu):
     b = sample_tokens(xd, temperature=1.0, top_k=0, top_p=0.95, seed=5).cpu()
     c = sample_tokens(xd, temperature=1.0, top_k=0, top_p=0.95, seed=6).cpu()
     assert torch.equal(a, b) and not torch.equal(a, c)
+
+
+def _both_forms(x, t, k, p, seed):
+    """The draws of qwen3_sample_bf16 and of qwen3_sample_ws_bf16 for the
+    same rows (x a (B, V) device view, t / k / p device arrays)."""
+    from qwen3_engine_from_scratch_amd import _lib
+
+    lib = _lib.load()
+    B, V = x.shape
+    dev = x.device
+    stream = _lib.stream_of(dev)
+    one = torch.empty(B, dtype=torch.int64, device=dev)
+    par = torch.full((B,), -7, dtype=torch.int64, device=dev)
+    _lib.check(lib.qwen3_sample_bf16(x.data_ptr(), x.stride(0), B, V, t.data_ptr(), k.data_ptr(),
+                                     p.data_ptr(), seed, one.data_ptr(), stream),
+               "qwen3_sample_bf16")
+    need = int(lib.qwen3_sample_workspace_bytes(B, V))
+    ws = torch.full((need,), 0xA5, dtype=torch.uint8, device=dev)  # stale contents are fine
+    _lib.check(lib.qwen3_sample_ws_bf16(x.data_ptr(), x.stride(0), B, V, t.data_ptr(),
+                                        k.data_ptr(), p.data_ptr(), seed, par.data_ptr(),
+                                        ws.data_ptr(), need, stream), "qwen3_sample_ws_bf16")
+    torch.cuda.synchronize()
+    return one.cpu(), par.cpu()
+
+
+@pytest.mark.parametrize("B,V,stride", [
+    (64, 151936, 151936),   # four parts per row
+    (1, 151936, 151936),    # eight parts
+    (128, 151936, 151936),  # two parts
+    (300, 151936, 151936),  # one part: the single-workgroup form
+    (16, 151935, 151937),   # rows not 16-byte aligned: element loads
+    (8, 20000, 20000),      # three rounds: three parts, the last one short
+    (8, 5000, 5000),        # under one round: one part
+])
+def test_parallel_form_draws_the_same_tokens(gpu, B, V, stride):
+    """Greedy rows, top-k + top-p, top-k alone (small and past the
+    candidate list), top-p alone, top-k >= vocab and several temperatures
+    in one batch: qwen3_sample_ws_bf16 draws exactly qwen3_sample_bf16's
+    tokens."""
+    g = torch.Generator().manual_seed(B + V)
+    base = torch.randn(B, stride, generator=g) * 2
+    if B >= 8:
+        base[1, : V // 2] = 1.5    # many ties at the top-k boundary
+        base[2] = base[2].round()  # a few hundred distinct values
+    xb = base.to(torch.bfloat16)
+    if B >= 16:  # NaNs of both signs (never drawn; greedy ranks them first)
+        bits = xb.view(torch.int16)
+        for r, sign_bit in ((0, 0), (3, 0), (6, 0), (9, 1), (14, 1)):
+            cols = torch.tensor([7, 8191, V // 3, V - 2])
+            bits[r, cols] = (0xFFC1 - 0x10000) if sign_bit else 0x7FC1
+    x = xb.to(gpu)[:, :V]
+    kinds = [(0.0, 50, 0.9), (0.8, 50, 0.9), (1.0, 1, 1.0), (1.0, 5000, 1.0), (0.7, 0, 0.9),
+             (1.2, V + 5, 0.95), (0.5, 3, 0.5), (2.0, 200, 0.99)]
+    t = torch.tensor([kinds[r % len(kinds)][0] for r in range(B)], device=gpu)
+    k = torch.tensor([kinds[r % len(kinds)][1] for r in range(B)], dtype=torch.int32, device=gpu)
+    p = torch.tensor([kinds[r % len(kinds)][2] for r in range(B)], device=gpu)
+    announce(f"sampling parallel form B={B} V={V} stride={stride}")
+    for seed in (1, 2):
+        one, par = _both_forms(x, t, k, p, seed)
+        assert torch.equal(one, par), f"B={B} V={V} seed={seed}: rows {(one != par).nonzero().view(-1)[:8].tolist()} differ"
