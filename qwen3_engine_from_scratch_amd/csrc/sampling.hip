@@ -185,12 +185,10 @@ struct Shared {
 // One part's results of the parallel passes (one per row and part, in the
 // workspace).
 struct alignas(16) PartOut {
-  uint32_t cnt[kHiBins];        // pass A: high-bin counts (sampled rows)
-  uint32_t lo_cnt[kLoBins];     // pass B: low-bin counts inside the boundary bin
-  uint32_t kmax;                // pass A: largest key
-  int32_t ncand;                // pass B: candidates written, -1 none
-  unsigned long long best;      // greedy rows: (key + 1) << 32 | ~index, the part's first maximum
-  unsigned long long cand[kCap];  // pass B: (key << 32) | token index
+  uint32_t kmax;                  // the part's largest key (kmax, ncand: one 8-byte load)
+  int32_t ncand;                  // candidates written, -1 none
+  unsigned long long best;        // greedy rows: (key + 1) << 32 | ~index, the first maximum
+  unsigned long long cand[kCap];  // (key << 32) | token index
 };
 
 // Parts per row of the parallel form: about one workgroup per CU over the
@@ -757,19 +755,119 @@ __global__ __launch_bounds__(kThreads) void sample_kernel(const uint16_t* logits
   uint32_t kmax = 0;
   bool from_list = false;  // the parts' lists stand for the row in passes A, B
   if constexpr (kPre) {
+    // One round trip: every part's (kmax, ncand) and, ahead of knowing the
+    // counts, entry tid % L of part tid / L (L = kThreads / P entries per
+    // part: all of a short list).
+    const int L = kThreads / P;
+    const int cpart = tid / L < P ? tid / L : P - 1;
+    const int coff = tid - (tid / L) * L;
+    const unsigned long long spec = rp[cpart].cand[coff];
+    unsigned long long hdr[kMaxParts];
+    part_values(P, 0ull, [&](int c) {
+      return *reinterpret_cast<const unsigned long long*>(&rp[c].kmax);
+    }, hdr);
+    // the entry's load stays here, in flight with the counts (the compiler
+    // would otherwise move it into the branch that uses it, after them)
+    asm volatile("" ::"v"(spec));
     int nc[kMaxParts];
-    part_values(P, 0, [&](int c) { return rp[c].ncand; }, nc);
-    uint32_t km[kMaxParts];
-    part_values(P, 0u, [&](int c) { return rp[c].kmax; }, km);
     int total = 0;
     from_list = true;
+    bool short_list = true;
 #pragma unroll
     for (int c = 0; c < kMaxParts; ++c) {
+      nc[c] = static_cast<int>(hdr[c] >> 32);
+      const uint32_t km = static_cast<uint32_t>(hdr[c]);
       from_list = from_list && nc[c] >= 0;
+      short_list = short_list && nc[c] <= L;
       total += nc[c] > 0 ? nc[c] : 0;
-      kmax = km[c] > kmax ? km[c] : kmax;
+      kmax = km > kmax ? km : kmax;
     }
     from_list = from_list && total <= kCap;
+    if (from_list && short_list) {  // uniform
+      // A short union (the usual case: k plus a few per part): one entry
+      // per thread, sorted by key (descending) and token index (ascending)
+      // with a bitonic network; the top-k list is then its first k
+      // positions and the top-p cut a prefix sum over them.  The same
+      // masses, limit and comparisons as passes C and D (a position is
+      // kept while the mass before it is within the limit; ties share one
+      // mass, so this is their rank rule), so the draw is the same.
+      // Sort keys: key << 32 | ~index (0 pads, below every entry).
+      int start_c = 0;  // the entries of the parts before this thread's
+#pragma unroll
+      for (int j = 0; j < kMaxParts; ++j) start_c += j < cpart ? nc[j] : 0;
+      if (tid / L < P && coff < nc[cpart])
+        sh.cand[start_c + coff] = (spec & 0xFFFFFFFF00000000ull) | (~static_cast<uint32_t>(spec));
+      if (tid < kThreads / 4) sh.cnt[tid] = 0;
+      __syncthreads();
+      unsigned long long x = tid < total ? sh.cand[tid] : 0ull;
+      if (total <= kThreads / 4) {  // uniform
+        // up to 256 entries: each entry's rank (the entries above it) from
+        // four threads that each compare it with a quarter of the list (LDS
+        // broadcast reads, no dependent chain), then a scatter to its rank
+        const int e = tid & (kThreads / 4 - 1), q = tid / (kThreads / 4);
+        const int j0 = (total * q) / 4, j1 = (total * (q + 1)) / 4;
+        if (e < total) {
+          const unsigned long long me = sh.cand[e];
+          int above = 0;
+          for (int j = j0; j < j1; j += 8) {  // eight reads in flight
+            unsigned long long v[8];
+#pragma unroll
+            for (int u = 0; u < 8; ++u) v[u] = sh.cand[j + u < j1 ? j + u : j0];
+#pragma unroll
+            for (int u = 0; u < 8; ++u) above += (j + u < j1 && v[u] > me) ? 1 : 0;
+          }
+          atomicAdd(&sh.cnt[e], static_cast<uint32_t>(above));
+        }
+        __syncthreads();
+        if (tid < total) sh.cand[kThreads + sh.cnt[tid]] = x;
+        __syncthreads();
+        x = tid < total ? sh.cand[kThreads + tid] : 0ull;
+      }
+      int n2 = 64;  // longer lists: a bitonic network over the next power of two
+      while (n2 < total) n2 <<= 1;
+      if (total <= kThreads / 4) n2 = 1;  // sorted already
+      for (int kb = 2; kb <= n2; kb <<= 1) {
+        for (int jb = kb >> 1; jb > 0; jb >>= 1) {
+          unsigned long long y;
+          if (jb >= 64) {  // uniform: across waves, through LDS
+            __syncthreads();
+            sh.cand[tid] = x;
+            __syncthreads();
+            y = sh.cand[tid ^ jb];
+          } else {
+            y = __shfl_xor(x, jb, 64);
+          }
+          const bool keep_max = ((tid & jb) == 0) == ((tid & kb) == 0);
+          x = keep_max ? (x > y ? x : y) : (x < y ? x : y);
+        }
+      }
+      const uint32_t key = static_cast<uint32_t>(x >> 32);
+      const uint32_t idx = ~static_cast<uint32_t>(x);
+      const bool in_k = tid < k && tid < total;
+      bool kept = in_k;
+      if (use_p) {
+        const float xmax = key_value(kmax) * inv_t;
+        unsigned long long wf = 0;
+        if (in_k) {
+          const float w = __expf(key_value(key) * inv_t - xmax);
+          wf = static_cast<unsigned long long>(static_cast<double>(w) * kFix + 0.5);
+        }
+        unsigned long long mass;
+        const unsigned long long before = block_scan_u64(wf, mass, sh);
+        const double limit = static_cast<double>(fmaxf(pcut, 0.f)) * static_cast<double>(mass);
+        kept = in_k && static_cast<double>(before) <= limit;
+      }
+      unsigned long long best = 0;
+      if (kept && key != 0) {  // as pass E's offer
+        const float sc = key_value(key) * inv_t + gumbel_of(draws4(seed, row, idx >> 2)[idx & 3]);
+        const uint32_t sb = __float_as_uint(sc);
+        const uint32_t so = (sb & 0x80000000u) ? ~sb : (sb | 0x80000000u);
+        best = (static_cast<unsigned long long>(so) << 32) | (~idx);
+      }
+      best = block_max_u64(best, sh);
+      if (tid == 0) out[row] = best ? static_cast<int64_t>(~static_cast<uint32_t>(best)) : 0;
+      return;
+    }
     if (from_list) {
       for (int i = tid; i < kHiBins; i += kThreads) sh.cnt[i] = 0;
       if (tid < kLoBins) sh.lo_cnt[tid] = 0;

@@ -167,12 +167,12 @@ def test_model_ops_reject_bad_arguments():
     assert lib.qwen3_sample_bf16(None, 151936, 4, 151936, None, None, None, 1, FAKE, None) == -1
     assert lib.qwen3_sample_bf16(FAKE, 151936, 0, 151936, None, None, None, 1, FAKE, None) == 0
     need = int(lib.qwen3_sample_workspace_bytes(64, 151936))
-    assert need == 64 * 4 * 49232          # 4 parts per row, one record per part
-    assert int(lib.qwen3_sample_workspace_bytes(16, 151936)) == 16 * 8 * 49232
-    assert int(lib.qwen3_sample_workspace_bytes(128, 151936)) == 128 * 2 * 49232
+    assert need == 64 * 4 * 32784          # 4 parts per row, one record per part
+    assert int(lib.qwen3_sample_workspace_bytes(16, 151936)) == 16 * 8 * 32784
+    assert int(lib.qwen3_sample_workspace_bytes(128, 151936)) == 128 * 2 * 32784
     assert int(lib.qwen3_sample_workspace_bytes(600, 151936)) == 0  # one workgroup per row
     assert int(lib.qwen3_sample_workspace_bytes(1, 1000)) == 0      # one round: one part
-    assert int(lib.qwen3_sample_workspace_bytes(1, 20000)) == 1 * 3 * 49232  # three rounds
+    assert int(lib.qwen3_sample_workspace_bytes(1, 20000)) == 1 * 3 * 32784  # three rounds
     assert lib.qwen3_sample_ws_bf16(FAKE, 151936, 64, 151936, None, None, None, 1, FAKE,
                                     FAKE, need - 16, None) == -1  # workspace too small
     assert lib.qwen3_sample_ws_bf16(FAKE, 151936, 64, 151936, None, None, None, 1, FAKE,

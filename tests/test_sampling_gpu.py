@@ -200,8 +200,11 @@ def test_parallel_form_draws_the_same_tokens(gpu, B, V, stride):
             cols = torch.tensor([7, 8191, V // 3, V - 2])
             bits[r, cols] = (0xFFC1 - 0x10000) if sign_bit else 0x7FC1
     x = xb.to(gpu)[:, :V]
+    # top-k 1 to 200: unions of at most 1,024 entries (the sorted form); 600:
+    # a longer union (the histogram passes over it); 5,000: lists past
+    # their capacity (the row passes)
     kinds = [(0.0, 50, 0.9), (0.8, 50, 0.9), (1.0, 1, 1.0), (1.0, 5000, 1.0), (0.7, 0, 0.9),
-             (1.2, V + 5, 0.95), (0.5, 3, 0.5), (2.0, 200, 0.99)]
+             (1.2, V + 5, 0.95), (0.5, 3, 0.5), (2.0, 200, 0.99), (0.9, 600, 0.95)]
     t = torch.tensor([kinds[r % len(kinds)][0] for r in range(B)], device=gpu)
     k = torch.tensor([kinds[r % len(kinds)][1] for r in range(B)], dtype=torch.int32, device=gpu)
     p = torch.tensor([kinds[r % len(kinds)][2] for r in range(B)], device=gpu)
