@@ -221,10 +221,16 @@ __device__ __forceinline__ unsigned long long block_max_u64(unsigned long long v
   __syncthreads();
   if ((threadIdx.x & 63) == 0) sh.best[threadIdx.x >> 6] = v;
   __syncthreads();
-  v = 0;
+  // lane w of every wave takes wave w's maximum: four steps instead of a
+  // sixteen-entry loop in every thread
+  const int lane = threadIdx.x & 63;
+  v = lane < kWaves ? sh.best[lane] : 0ull;
 #pragma unroll
-  for (int w = 0; w < kWaves; ++w) v = sh.best[w] > v ? sh.best[w] : v;
-  return v;
+  for (int m = 1; m < kWaves; m <<= 1) {
+    const unsigned long long o = __shfl_xor(v, m, 64);
+    v = o > v ? o : v;
+  }
+  return __shfl(v, 0, 64);
 }
 
 // Appends (key, index) of the lanes where q holds to the block's candidate
@@ -272,6 +278,24 @@ __device__ __forceinline__ void append_round(const bool (&q)[8], const uint32_t 
   }
 }
 
+// The waves' partials (part[w] of wave w, in LDS) combined in one wave:
+// lane w takes part[w], a four-step scan gives every wave the sum of the
+// waves before it and the total (instead of a sixteen-entry loop in every
+// thread).
+template <typename T>
+__device__ __forceinline__ void scan_waves(const T* part, T& before, T& total) {
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const T x = lane < kWaves ? part[lane] : T(0);
+  T incl = x;
+#pragma unroll
+  for (int o = 1; o < kWaves; o <<= 1) {
+    const T y = __shfl_up(incl, o, 64);
+    if (lane >= o) incl += y;
+  }
+  total = __shfl(incl, kWaves - 1, 64);
+  before = __shfl(incl - x, wave, 64);
+}
+
 // Block-wide sums; every thread gets the result.
 __device__ __forceinline__ int block_sum_int(int v, Shared& sh) {
 #pragma unroll
@@ -279,9 +303,8 @@ __device__ __forceinline__ int block_sum_int(int v, Shared& sh) {
   __syncthreads();
   if ((threadIdx.x & 63) == 0) sh.wsum[threadIdx.x >> 6] = v;
   __syncthreads();
-  int t = 0;
-#pragma unroll
-  for (int w = 0; w < kWaves; ++w) t += sh.wsum[w];
+  int before, t;
+  scan_waves(sh.wsum, before, t);
   return t;
 }
 
@@ -298,13 +321,8 @@ __device__ __forceinline__ int block_scan_int(int v, int& total, Shared& sh) {
   __syncthreads();
   if (lane == 63) sh.wsum[wave] = incl;
   __syncthreads();
-  int before = 0;
-  total = 0;
-#pragma unroll
-  for (int w = 0; w < kWaves; ++w) {
-    if (w < wave) before += sh.wsum[w];
-    total += sh.wsum[w];
-  }
+  int before;
+  scan_waves(sh.wsum, before, total);
   return before + incl - v;
 }
 
@@ -322,13 +340,8 @@ __device__ __forceinline__ unsigned long long block_scan_u64(unsigned long long 
   __syncthreads();
   if (lane == 63) sh.wmass[wave] = incl;
   __syncthreads();
-  unsigned long long before = 0;
-  total = 0;
-#pragma unroll
-  for (int w = 0; w < kWaves; ++w) {
-    if (w < wave) before += sh.wmass[w];
-    total += sh.wmass[w];
-  }
+  unsigned long long before;
+  scan_waves(sh.wmass, before, total);
   return before + incl - v;
 }
 
@@ -424,17 +437,25 @@ __device__ __forceinline__ void for_each_round_in(const uint16_t* p, int64_t lo,
 // Scans the low-bit count histogram from the top: returns the bin where the
 // running count (starting at `above`) first reaches `need`, and the count
 // strictly above that bin.
+// Every lane of a wave gets the result: lane i < 16 takes bin 15 - i, a
+// four-step scan gives the counts from the top, a ballot the crossing.
 __device__ __forceinline__ int find_count_bin(const uint32_t* h, int64_t need, int64_t& above) {
-  int64_t run = above;
-  for (int bin = kLoBins - 1; bin >= 0; --bin) {
-    if (run + h[bin] >= need) {
-      above = run;
-      return bin;
-    }
-    run += h[bin];
+  const int lane = threadIdx.x & 63;
+  const int64_t c = lane < kLoBins ? static_cast<int64_t>(h[kLoBins - 1 - lane]) : 0;
+  int64_t incl = c;
+#pragma unroll
+  for (int o = 1; o < kLoBins; o <<= 1) {
+    const int64_t y = __shfl_up(incl, o, 64);
+    if (lane >= o) incl += y;
   }
-  above = run;
-  return 0;
+  const unsigned long long m = __ballot(lane < kLoBins && above + incl >= need);
+  if (m == 0ull) {  // not reached: every count is above, bin 0
+    above += __shfl(incl, kLoBins - 1, 64);
+    return 0;
+  }
+  const int i = __ffsll(static_cast<long long>(m)) - 1;
+  above += __shfl(incl - c, i, 64);
+  return kLoBins - 1 - i;
 }
 
 // The same over the 4096 high bins, by the whole block: thread t sums bins
@@ -619,17 +640,43 @@ __global__ __launch_bounds__(kThreads) void sample_part_kernel(const uint16_t* l
       t_lo = static_cast<uint32_t>(find_count_bin_block(sh.cnt, kreq, above, sh)) << kLoBits;
     }
     visit([&](int64_t i0, const uint32_t* b, auto full) {
-      // most rounds keep nothing of the wave: a whole round is passed over
-      // on its raw maximum (a NaN there only sends it to the exact test)
-      if constexpr (decltype(full)::value)
-        if (__ballot(round_raw_max(b) >= t_lo) == 0ull) return;
       bool q[8], any = false;
       uint32_t keys[8];
+      bool exact = true;
+      if constexpr (decltype(full)::value) {
+        // most rounds keep nothing of the wave: a whole round is passed
+        // over on its raw maximum; without a positive NaN in the thread's
+        // round (and with t_lo above every negative NaN's raw key) the raw
+        // keys are the keys for the test
+        uint32_t r2[4], m = 0;
 #pragma unroll
-      for (int e = 0; e < 8; ++e) {
-        keys[e] = okey(b[e]);
-        q[e] = (full || i0 + e < hi) && keys[e] >= t_lo;
-        any = any || q[e];
+        for (int j = 0; j < 4; ++j) {
+          r2[j] = raw_keys2(b[2 * j] | (b[2 * j + 1] << 16));
+          m = max_u16x2(m, r2[j]);
+        }
+        const uint32_t rmx = (m & 0xFFFFu) > (m >> 16) ? (m & 0xFFFFu) : (m >> 16);
+        if (__ballot(rmx >= t_lo) == 0ull) return;
+        if (rmx <= 0xFF80u && t_lo > 0x7Eu) {
+          exact = false;
+#pragma unroll
+          for (int j = 0; j < 4; ++j) {
+            keys[2 * j] = r2[j] & 0xFFFFu;
+            keys[2 * j + 1] = r2[j] >> 16;
+          }
+#pragma unroll
+          for (int e = 0; e < 8; ++e) {
+            q[e] = keys[e] >= t_lo;
+            any = any || q[e];
+          }
+        }
+      }
+      if (exact) {
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          keys[e] = okey(b[e]);
+          q[e] = (full || i0 + e < hi) && keys[e] >= t_lo;
+          any = any || q[e];
+        }
       }
       if (__ballot(any) == 0ull) return;
       append_round(q, keys, i0, sh);

@@ -196,7 +196,9 @@ def test_parallel_form_draws_the_same_tokens(gpu, B, V, stride):
     xb = base.to(torch.bfloat16)
     if B >= 16:  # NaNs of both signs (never drawn; greedy ranks them first)
         bits = xb.view(torch.int16)
-        for r, sign_bit in ((0, 0), (3, 0), (6, 0), (9, 1), (14, 1)):
+        for r, sign_bit in ((0, 0), (3, 0), (6, 0), (9, 1), (10, 1), (14, 1), (16, 1)):
+            if r >= B:
+                continue
             cols = torch.tensor([7, 8191, V // 3, V - 2])
             bits[r, cols] = (0xFFC1 - 0x10000) if sign_bit else 0x7FC1
     x = xb.to(gpu)[:, :V]
