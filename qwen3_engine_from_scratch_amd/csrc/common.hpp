@@ -109,4 +109,36 @@ inline bool aligned16(const void* p) {
   return (reinterpret_cast<uintptr_t>(p) & 15u) == 0;
 }
 
+// Lane moves inside a 16-lane DPP row: one full-rate VALU instruction
+// each, where __shfl_xor compiles to an LDS permute (ds_bpermute) and its
+// round trip.  Controls: quad_perm [1,0,3,2] (lane ^ 1), [2,3,0,1]
+// (lane ^ 2), row_half_mirror (lane i <-> 7 - i within eight), row_mirror
+// (lane i <-> 15 - i), row_ror:8 (lane ^ 8 within sixteen).
+enum : int {
+  kDppXor1 = 0xB1,
+  kDppXor2 = 0x4E,
+  kDppHalfMirror = 0x141,
+  kDppMirror = 0x140,
+  kDppRor8 = 0x128,
+};
+template <int kCtrl>
+__device__ __forceinline__ uint32_t dpp_u32(uint32_t v) {
+  return static_cast<uint32_t>(
+      __builtin_amdgcn_mov_dpp(static_cast<int>(v), kCtrl, 0xF, 0xF, false));
+}
+template <int kCtrl>
+__device__ __forceinline__ float dpp_f32(float v) {
+  return __uint_as_float(dpp_u32<kCtrl>(__float_as_uint(v)));
+}
+// Sum over the 16 lanes of a row.  After the two quad steps every lane of
+// a quad holds the quad's sum, so the mirrors pair the same values as a xor
+// butterfly over 4 and 8: the result has the butterfly's bits.
+__device__ __forceinline__ float row16_sum(float v) {
+  v += dpp_f32<kDppXor1>(v);
+  v += dpp_f32<kDppXor2>(v);
+  v += dpp_f32<kDppHalfMirror>(v);
+  v += dpp_f32<kDppMirror>(v);
+  return v;
+}
+
 }  // namespace q3

@@ -163,8 +163,8 @@ __global__ __launch_bounds__(kWaves * 64) void decode_linear_kernel(LinArgs a) {
       } else {
         for (int t = part; t < a.ss_in_tiles; t += 4) s += sp[t];
       }
-      s += __shfl_xor(s, 1, 64);
-      s += __shfl_xor(s, 2, 64);
+      s += q3::dpp_f32<q3::kDppXor1>(s);  // lane ^ 1
+      s += q3::dpp_f32<q3::kDppXor2>(s);  // lane ^ 2
       if (part == 0) rms_s[threadIdx.x >> 2] = 1.f / sqrtf(s / static_cast<float>(a.K) + a.eps);
     }
     __syncthreads();
@@ -238,8 +238,7 @@ __global__ __launch_bounds__(kWaves * 64) void decode_linear_kernel(LinArgs a) {
         a.res_out[static_cast<int64_t>(row) * a.res_out_s + col] = to_bf16(h);
       }
       float sq = __fmul_rn(h, h);
-#pragma unroll
-      for (int m = 1; m < 16; m <<= 1) sq = __fadd_rn(sq, __shfl_xor(sq, m, 16));
+      sq = q3::row16_sum(sq);
       if (live && r16 == 0) a.ss_out[static_cast<int64_t>(row) * (a.N / kTile) + tile] = sq;
     }
   }
@@ -316,8 +315,8 @@ __global__ __launch_bounds__(kWaves64 * 64) void gate_up64_kernel(LinArgs a) {
     } else {
       for (int t = part; t < a.ss_in_tiles; t += 4) s += sp[t];
     }
-    s += __shfl_xor(s, 1, 64);
-    s += __shfl_xor(s, 2, 64);
+    s += q3::dpp_f32<q3::kDppXor1>(s);  // lane ^ 1
+    s += q3::dpp_f32<q3::kDppXor2>(s);  // lane ^ 2
     if (part == 0) rms_s[tid >> 2] = 1.f / sqrtf(s / static_cast<float>(a.K) + a.eps);
   }
   __syncthreads();

@@ -159,8 +159,8 @@ __global__ __launch_bounds__(kThreadsQ) void qkv_rope_kernel(QkvArgs a) {
     } else {
       for (int t = part; t < a.ss_tiles; t += 4) s += sp[t];
     }
-    s += __shfl_xor(s, 1, 64);
-    s += __shfl_xor(s, 2, 64);
+    s += q3::dpp_f32<q3::kDppXor1>(s);  // lane ^ 1
+    s += q3::dpp_f32<q3::kDppXor2>(s);  // lane ^ 2
     if (part == 0) rms_s[lane >> 2] = 1.f / sqrtf(s / static_cast<float>(a.K) + a.eps);
   } else if (wave == 1 && lane < kRowsPerBlock) {
     const int t = rb * 16 + lane;
@@ -284,15 +284,14 @@ __global__ __launch_bounds__(kThreadsQ) void qkv_rope_kernel(QkvArgs a) {
   float ss = 0.f;
 #pragma unroll
   for (int e = 0; e < 8; ++e) ss = __fadd_rn(ss, __fmul_rn(x[e], x[e]));
-#pragma unroll
-  for (int m = 1; m < 16; m <<= 1) ss += __shfl_xor(ss, m, 16);
+  ss = q3::row16_sum(ss);
   const float rmsh = 1.f / sqrtf(ss / static_cast<float>(kD) + a.head_eps);
   uint32_t np[4], pp[4];
 #pragma unroll
   for (int e = 0; e < 4; ++e)
     np[e] = q3::pack_bf16x2((x[2 * e] * rmsh) * w[2 * e], (x[2 * e + 1] * rmsh) * w[2 * e + 1]);
 #pragma unroll
-  for (int e = 0; e < 4; ++e) pp[e] = static_cast<uint32_t>(__shfl_xor(static_cast<int>(np[e]), 8, 16));
+  for (int e = 0; e < 4; ++e) pp[e] = q3::dpp_u32<q3::kDppRor8>(np[e]);  // lane j ^ 8
   const float sign = j < 8 ? -1.f : 1.f;  // rotate_half: (-x2, x1)
   q3::u32x4 out = {0u, 0u, 0u, 0u};
   if (ok_pos) {

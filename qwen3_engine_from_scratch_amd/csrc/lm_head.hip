@@ -57,6 +57,21 @@ __device__ __forceinline__ unsigned long long umax64(unsigned long long a, unsig
   return a > b ? a : b;
 }
 
+// Maximum over the 16 lanes of a DPP row (a maximum does not depend on
+// the pairing; each step moves both halves of the key with DPP).
+template <int kCtrl>
+__device__ __forceinline__ unsigned long long dpp_u64(unsigned long long v) {
+  const uint32_t lo = q3::dpp_u32<kCtrl>(static_cast<uint32_t>(v));
+  const uint32_t hi = q3::dpp_u32<kCtrl>(static_cast<uint32_t>(v >> 32));
+  return (static_cast<unsigned long long>(hi) << 32) | lo;
+}
+__device__ __forceinline__ unsigned long long row16_max64(unsigned long long v) {
+  v = umax64(v, dpp_u64<q3::kDppXor1>(v));
+  v = umax64(v, dpp_u64<q3::kDppXor2>(v));
+  v = umax64(v, dpp_u64<q3::kDppHalfMirror>(v));
+  return umax64(v, dpp_u64<q3::kDppMirror>(v));
+}
+
 __global__ __launch_bounds__(kThreadsH) void lm_head_argmax_kernel(HeadArgs a) {
   extern __shared__ uint16_t a_s[];  // row r at a_s + r * pitch
   __shared__ float rms_s[kMaxRows];
@@ -127,8 +142,8 @@ __global__ __launch_bounds__(kThreadsH) void lm_head_argmax_kernel(HeadArgs a) {
     } else {
       for (int t = part; t < a.ss_tiles; t += 4) s += sp[t];
     }
-    s += __shfl_xor(s, 1, 64);
-    s += __shfl_xor(s, 2, 64);
+    s += q3::dpp_f32<q3::kDppXor1>(s);  // lane ^ 1
+    s += q3::dpp_f32<q3::kDppXor2>(s);  // lane ^ 2
     if (part == 0) rms_s[tid >> 2] = 1.f / sqrtf(s / static_cast<float>(a.K) + a.eps);
   }
   __syncthreads();
@@ -216,8 +231,7 @@ __global__ __launch_bounds__(kThreadsH) void lm_head_argmax_kernel(HeadArgs a) {
   for (int rb = 0; rb < kRowBlocks; ++rb)
 #pragma unroll
     for (int i = 0; i < 4; ++i)
-#pragma unroll
-      for (int m = 1; m < 16; m <<= 1) best[rb][i] = umax64(best[rb][i], __shfl_xor(best[rb][i], m, 64));
+      best[rb][i] = row16_max64(best[rb][i]);
   if (r16 == 0) {
 #pragma unroll
     for (int rb = 0; rb < kRowBlocks; ++rb)

@@ -185,8 +185,7 @@ __global__ __launch_bounds__(256) void pre_attention_kernel(PreAttnArgs a) {
     float ss = 0.f;
 #pragma unroll
     for (int e = 0; e < 8; ++e) ss = __fadd_rn(ss, __fmul_rn(x[e], x[e]));
-#pragma unroll
-    for (int m = 1; m < kLanesPerRow; m <<= 1) ss += __shfl_xor(ss, m, kLanesPerRow);
+    ss = q3::row16_sum(ss);
     // 1 / sqrt with IEEE sqrt and division: the hardware rsqrt's extra ulp
     // moves some outputs by two bf16 ulps from the reference's rsqrt.
     const float rms = 1.f / sqrtf(ss / static_cast<float>(kD) + a.eps);
@@ -197,8 +196,7 @@ __global__ __launch_bounds__(256) void pre_attention_kernel(PreAttnArgs a) {
     for (int e = 0; e < 4; ++e)
       np[e] = q3::pack_bf16x2((x[2 * e] * rms) * w[2 * e], (x[2 * e + 1] * rms) * w[2 * e + 1]);
 #pragma unroll
-    for (int e = 0; e < 4; ++e)
-      pp[e] = static_cast<uint32_t>(__shfl_xor(static_cast<int>(np[e]), 8, kLanesPerRow));
+    for (int e = 0; e < 4; ++e) pp[e] = q3::dpp_u32<q3::kDppRor8>(np[e]);  // lane j ^ 8
 
     q3::u32x4 out = {0u, 0u, 0u, 0u};
     if (ok_pos) {
