@@ -193,8 +193,7 @@ __device__ __forceinline__ void compute_chunk(Chunk& c, float scale_log2, int hi
       if (!ok) c.v[i][r] = q3::u32x4{0u, 0u, 0u, 0u};
     }
   }
-  mx = fmaxf(mx, q3::shfl_xor(mx, 16));
-  mx = fmaxf(mx, q3::shfl_xor(mx, 32));
+  mx = q3::max_xor32(q3::max_xor16(mx));
   const float m_new = fmaxf(st.m, mx);
   const float m_use = m_new == q3::kNegInf ? 0.f : m_new;
   const float alpha = q3::fast_exp2(st.m - m_use);
@@ -248,8 +247,7 @@ __device__ __forceinline__ void compute_chunk(Chunk& c, float scale_log2, int hi
 // Completes the per-column denominator (lanes of one column hold disjoint
 // token subsets) and returns 1/l (0 for an empty column).
 __device__ __forceinline__ float finish_l(SoftmaxState& st) {
-  st.l += q3::shfl_xor(st.l, 16);
-  st.l += q3::shfl_xor(st.l, 32);
+  st.l = q3::sum_xor32(q3::sum_xor16(st.l));
   return st.l > 0.f ? 1.f / st.l : 0.f;
 }
 
@@ -658,8 +656,7 @@ void paged_decode_grid_kernel(DecodeArgs a) {
     compute_chunk(cbuf, a.scale_log2, hi, qv, st);
     issue(cbuf);
   }
-  st.l += q3::shfl_xor(st.l, 16);
-  st.l += q3::shfl_xor(st.l, 32);
+  st.l = q3::sum_xor32(q3::sum_xor16(st.l));
 
   __shared__ float s_m[kWaves][kMaxG];
   __shared__ float s_l[kWaves][kMaxG];
