@@ -75,8 +75,9 @@ __global__ __launch_bounds__(256) void add_rms_norm_kernel(NormArgs a) {
       ss = __fadd_rn(ss, __fmul_rn(hi, hi));
     }
   }
-#pragma unroll
-  for (int m = 1; m < kWave; m <<= 1) ss += __shfl_xor(ss, m, kWave);
+  // the xor butterfly over the wave's 64 lanes, with the same pairings (and
+  // bits) from DPP and permlane swaps instead of LDS permutes
+  ss = q3::sum_xor32(q3::sum_xor16(q3::row16_sum(ss)));
   const float rms = 1.f / sqrtf(ss / static_cast<float>(a.hidden) + a.eps);
 #pragma unroll
   for (int c = 0; c < CPL; ++c) {
