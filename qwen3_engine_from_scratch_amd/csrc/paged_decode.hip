@@ -48,7 +48,9 @@ constexpr int kWin = 64;       // block-table entries held per window (one per l
 constexpr int kStreamMaxB = 2048;       // batch entries tabulated in LDS
 constexpr int kStreamWgPerCu = 2;       // resident workgroups per CU (2 waves/SIMD)
 constexpr int kStreamMaxWgs = 1024;     // workspace sized for up to 512 CUs
-constexpr int kMinTilesPerWave = 8;
+// Fewest tiles a wave streams: its two load batches, both issued before the
+// first is computed, so a small batch costs one tile round trip per wave.
+constexpr int kMinTilesPerWave = 2 * kChunk;
 // Grid path (large batches).
 constexpr int kGridTilesPerWave = 32;
 constexpr int kGridTilesPerPart = kGridTilesPerWave * kWaves;
