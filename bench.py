@@ -229,6 +229,42 @@ def read_reference(nbytes, dev, reps=5):
             "kernel": f"torch.amax over {nbytes} bytes of int64"}
 
 
+def stream_read_reference(nbytes, dev, nontemporal=True, reps=5):
+    """What the library's streaming read reference (qwen3_hbm_read_reference:
+    16-byte loads over a persistent grid, non-temporal like the decode's K/V
+    loads or plain, no other work) reaches on nbytes: the device's read
+    ceiling for the decode call's byte count."""
+    import torch
+
+    from qwen3_engine_from_scratch_amd import _lib
+
+    lib = _lib.load()
+    n = nbytes // 16 * 16
+    buf = torch.ones(n // 8, dtype=torch.int64, device=dev)
+    sink = torch.zeros(4, dtype=torch.int32, device=dev)
+    stream = _lib.stream_of(dev)
+
+    def call():
+        _lib.check(lib.qwen3_hbm_read_reference(buf.data_ptr(), n, 1 if nontemporal else 0,
+                                                sink.data_ptr(), stream),
+                   "qwen3_hbm_read_reference")
+
+    call()
+    torch.cuda.synchronize()
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    start.record()
+    for _ in range(reps):
+        call()
+    end.record()
+    torch.cuda.synchronize()
+    ms = start.elapsed_time(end) / reps
+    del buf
+    torch.cuda.empty_cache()
+    return {"GB/s": round(n / (ms * 1e-3) / 1e9, 1), "ms": round(ms, 5),
+            "kernel": f"qwen3_hbm_read_reference over {n} bytes, "
+                      f"{'non-temporal' if nontemporal else 'plain'} 16-byte loads"}
+
+
 def seeded_lengths(n: int, lo: int, hi: int, seed: int = 0) -> list:
     """n lengths uniform in [lo, hi] from a seeded CPU generator."""
     import torch
@@ -877,6 +913,9 @@ def main(argv=None):
         del res
         torch.cuda.empty_cache()
         line["roofline"]["read_reference"] = read_reference(nbytes, dev)
+        line["roofline"]["stream_read_reference"] = stream_read_reference(nbytes, dev)
+        line["roofline"]["frac_of_stream_read"] = round(
+            line["roofline"]["achieved"] / line["roofline"]["stream_read_reference"]["GB/s"], 4)
         if args.workload == "config3" and not args.no_long_context:
             long_args = argparse.Namespace(**{**vars(args), "workload": "config4"})
             r4 = bench_decode(long_args, dev)

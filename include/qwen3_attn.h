@@ -322,6 +322,18 @@ int qwen3_qk_norm_rope_slots_bf16(const void* q, const int64_t q_strides[2],
                                   int num_heads, int num_kv_heads, int head_dim,
                                   int block_size, void* stream);
 
+/* ------------------------------------------------------------------------
+ * Streaming read reference (no counterpart in the reference engine; for the
+ * measurement of the HBM-bound entry points above): reads `bytes` bytes
+ * (a multiple of 16) at `src` with 16-byte loads, non-temporal when
+ * `nontemporal` is nonzero (the load type of the decode's K/V stream),
+ * across a persistent grid, and computes nothing from them.  `sink` is a
+ * 16-byte aligned 4-byte device word the kernel may write.  Its time per
+ * call is the device's read rate for that many bytes.
+ * ------------------------------------------------------------------------ */
+int qwen3_hbm_read_reference(const void* src, int64_t bytes, int nontemporal, void* sink,
+                             void* stream);
+
 #ifdef __cplusplus
 }
 #endif

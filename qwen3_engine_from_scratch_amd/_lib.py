@@ -23,6 +23,7 @@ _i64 = ctypes.c_int64
 _SIGNATURES = {
     "qwen3_attn_last_error": (ctypes.c_char_p, []),
     "qwen3_attn_abi_version": (_i, []),
+    "qwen3_hbm_read_reference": (_i, [_vp, _i64, _i, _vp, _vp]),
     "qwen3_paged_decode_workspace_bytes": (ctypes.c_size_t, [_i, _i, _i, _i64, _i]),
     "qwen3_paged_decode_bf16": (
         _i,
@@ -113,7 +114,7 @@ _SIGNATURES = {
     ),
 }
 
-ABI_VERSION = 6
+ABI_VERSION = 7
 
 _lib = None
 

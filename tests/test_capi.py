@@ -248,3 +248,13 @@ def test_wrappers_refuse_cpu_tensors():
     cu = torch.tensor([0, 2], dtype=torch.int32)
     with pytest.raises(RuntimeError, match="no CPU fallback"):
         flash_attention_prefill(q, q[:, :8], q[:, :8], cu, 0.088, 16, 8, 128, max_seqlen=2)
+
+
+def test_hbm_read_reference_rejects_bad_arguments():
+    lib = _lib.load()
+    assert lib.qwen3_hbm_read_reference(None, 1 << 20, 1, FAKE, None) == -1
+    assert lib.qwen3_hbm_read_reference(FAKE, 1 << 20, 1, None, None) == -1
+    assert lib.qwen3_hbm_read_reference(FAKE, (1 << 20) + 8, 1, FAKE, None) == -1  # not 16 B units
+    assert lib.qwen3_hbm_read_reference(FAKE, -16, 0, FAKE, None) == -1
+    assert lib.qwen3_hbm_read_reference(FAKE + 8, 1 << 20, 0, FAKE, None) == -2   # misaligned
+    assert lib.qwen3_hbm_read_reference(FAKE, 0, 1, FAKE, None) == 0              # nothing to read
