@@ -265,6 +265,40 @@ def stream_read_reference(nbytes, dev, nontemporal=True, reps=5):
                       f"{'non-temporal' if nontemporal else 'plain'} 16-byte loads"}
 
 
+def mfma_rate_reference(dev, iters=2000, reps=5):
+    """What the library's matrix-core rate reference (qwen3_mfma_rate_reference:
+    back-to-back bf16 32x32x16 MFMAs from registers, two waves per SIMD as in
+    the prefill kernel, no memory traffic) sustains: the practical bf16 ceiling
+    at the clock the device holds under matrix-core load."""
+    import ctypes
+
+    import torch
+
+    from qwen3_engine_from_scratch_amd import _lib
+
+    lib = _lib.load()
+    sink = torch.zeros(4, dtype=torch.int32, device=dev)
+    flops = ctypes.c_int64(0)
+    stream = _lib.stream_of(dev)
+
+    def call():
+        _lib.check(lib.qwen3_mfma_rate_reference(iters, sink.data_ptr(), ctypes.byref(flops),
+                                                 stream), "qwen3_mfma_rate_reference")
+
+    call()
+    torch.cuda.synchronize()
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    start.record()
+    for _ in range(reps):
+        call()
+    end.record()
+    torch.cuda.synchronize()
+    ms = start.elapsed_time(end) / reps
+    return {"TFLOP/s": round(flops.value / (ms * 1e-3) / 1e12, 1), "ms": round(ms, 5),
+            "kernel": f"qwen3_mfma_rate_reference, {flops.value} flop per call "
+                      "(bf16 32x32x16 MFMAs, two waves per SIMD, no memory traffic)"}
+
+
 def seeded_lengths(n: int, lo: int, hi: int, seed: int = 0) -> list:
     """n lengths uniform in [lo, hi] from a seeded CPU generator."""
     import torch
@@ -587,6 +621,7 @@ def bench_prefill(args, dev):
         s_evt = time_graph(sstep, args.steps, args.warmup)
         flops = 4 * 128 * 16 * sum(L * L for L in lens)
         tflops = flops / (s_evt * 1e-3) / 1e12
+        mref = mfma_rate_reference(dev)
         log(f"prefill (steady, 8x4096 non-causal): {s_evt * 1e3:.1f} us/call, {tflops:.1f} TFLOP/s")
         return {"workload": "varlen non-causal prefill, 8 x 4096 tokens, 16/8 heads, head_dim 128, bf16",
                 "value": round(tflops, 2), "unit": "TFLOP/s", "ms_per_step": round(s_evt, 5),
@@ -594,7 +629,9 @@ def bench_prefill(args, dev):
                 "flops": flops,
                 "roofline": {"bound": "mfma", "achieved": round(tflops, 2),
                              "peak": MFMA_BF16_PEAK_TFLOPS, "unit": "TFLOP/s",
-                             "frac": round(tflops / MFMA_BF16_PEAK_TFLOPS, 4), "traffic": None}}
+                             "frac": round(tflops / MFMA_BF16_PEAK_TFLOPS, 4), "traffic": None,
+                             "mfma_rate_reference": mref,
+                             "frac_of_mfma_rate": round(tflops / mref["TFLOP/s"], 4)}}
 
     # Qwen3-0.6B batch: N(0,1) projections, QK-RMSNorm (weights 1 + 0.1 N(0,1))
     # and RoPE at positions 0..L-1 applied by the fused pre-attention kernel.
@@ -631,6 +668,7 @@ def bench_prefill(args, dev):
     cold_ms = time_steps_flushed(step, args.steps, args.warmup, dev)
     flops = 2 * 128 * 16 * sum(L * (L + 1) for L in lens)
     tflops = flops / (evt_ms * 1e-3) / 1e12
+    mref = mfma_rate_reference(dev)
     log(f"prefill: {evt_ms * 1e3:.1f} us/call back to back ({cold_ms * 1e3:.1f} flushed, "
         f"{eager_ms * 1e3:.1f} eager loop), {tflops:.1f} TFLOP/s")
 
@@ -667,7 +705,9 @@ def bench_prefill(args, dev):
                         "peak": MFMA_BF16_PEAK_TFLOPS, "unit": "TFLOP/s",
                         "frac": round(tflops / MFMA_BF16_PEAK_TFLOPS, 4),
                         "traffic": profiled_traffic(PREFILL_PROFILE),
-                        "traffic_source": f"profiles/{PREFILL_PROFILE}"},
+                        "traffic_source": f"profiles/{PREFILL_PROFILE}",
+                        "mfma_rate_reference": mref,
+                        "frac_of_mfma_rate": round(tflops / mref["TFLOP/s"], 4)},
            "slot_write": {"GB/s": round(wgbs, 1), "frac_hbm_peak": round(wgbs / HBM_PEAK_GBS, 4),
                           "ms_per_step": round(w_evt, 5),
                           "ms_per_step_back_to_back": round(w_hot, 5), "bytes": wbytes,

@@ -334,6 +334,16 @@ int qwen3_qk_norm_rope_slots_bf16(const void* q, const int64_t q_strides[2],
 int qwen3_hbm_read_reference(const void* src, int64_t bytes, int nontemporal, void* sink,
                              void* stream);
 
+/* Matrix-core rate reference (no counterpart in the reference engine; for the
+ * measurement of the prefill kernel): every wave of a persistent grid (two
+ * 256-thread workgroups per CU) issues iters x 16 back-to-back
+ * mfma_f32_32x32x16_bf16 products from registers, with no memory traffic.
+ * *flops (host) receives the launch's flop count; `sink` is a 16-byte
+ * aligned 4-byte device word the kernel may write.  Its time per call gives
+ * the bf16 rate the device sustains, at the clock it holds under that load.
+ * iters in [1, 2^24]. */
+int qwen3_mfma_rate_reference(int iters, void* sink, int64_t* flops, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -24,6 +24,7 @@ _SIGNATURES = {
     "qwen3_attn_last_error": (ctypes.c_char_p, []),
     "qwen3_attn_abi_version": (_i, []),
     "qwen3_hbm_read_reference": (_i, [_vp, _i64, _i, _vp, _vp]),
+    "qwen3_mfma_rate_reference": (_i, [_i, _vp, _c_i64p, _vp]),
     "qwen3_paged_decode_workspace_bytes": (ctypes.c_size_t, [_i, _i, _i, _i64, _i]),
     "qwen3_paged_decode_bf16": (
         _i,

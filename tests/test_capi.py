@@ -258,3 +258,13 @@ def test_hbm_read_reference_rejects_bad_arguments():
     assert lib.qwen3_hbm_read_reference(FAKE, -16, 0, FAKE, None) == -1
     assert lib.qwen3_hbm_read_reference(FAKE + 8, 1 << 20, 0, FAKE, None) == -2   # misaligned
     assert lib.qwen3_hbm_read_reference(FAKE, 0, 1, FAKE, None) == 0              # nothing to read
+
+
+def test_mfma_rate_reference_rejects_bad_arguments():
+    lib = _lib.load()
+    flops = ctypes.c_int64(0)
+    assert lib.qwen3_mfma_rate_reference(0, FAKE, ctypes.byref(flops), None) == -1
+    assert lib.qwen3_mfma_rate_reference((1 << 24) + 1, FAKE, ctypes.byref(flops), None) == -1
+    assert lib.qwen3_mfma_rate_reference(10, None, ctypes.byref(flops), None) == -1
+    assert lib.qwen3_mfma_rate_reference(10, FAKE, None, None) == -1
+    assert lib.qwen3_mfma_rate_reference(10, FAKE + 4, ctypes.byref(flops), None) == -2
