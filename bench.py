@@ -337,7 +337,7 @@ def bench_decode(args, dev):
     log(f"decode inputs: B={len(lens)} sumL={sum(lens)}")
     t = decode_inputs(lens, hq, hkv, dev)
     out = torch.empty_like(t["q"])
-    ws = torch.empty(paged_decode_workspace_bytes(len(lens), hq, 128, t["bt"].shape[1], 16),
+    ws = torch.empty(paged_decode_workspace_bytes(len(lens), hq, hkv, 128, t["bt"].shape[1], 16),
                      dtype=torch.uint8, device=dev)
 
     def step():

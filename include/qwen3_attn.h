@@ -91,17 +91,18 @@ int qwen3_attn_abi_version(void);
  *   row_ids    int32 (B,) or NULL (identity)
  *   workspace  device scratch of at least qwen3_paged_decode_workspace_bytes()
  *              bytes, 16-byte aligned (split-KV partials); its size depends
- *              only on (B, num_heads, head_dim, max_pages, block_size), never
- *              on the live lengths, so one launch shape serves a captured
- *              graph.  Its contents need no initialisation.
+ *              only on (B, num_heads, num_kv_heads, head_dim, max_pages,
+ *              block_size) and the current device's CU count, never on the
+ *              live lengths, so one launch shape serves a captured graph.
+ *              Its contents need no initialisation.
  * Supported: head_dim 128, block_size a multiple of 16,
  *            num_heads / num_kv_heads in [1, 16]; q, K, V and out rows
  *            16-byte aligned (strides multiples of 8 elements).
  * Launches two kernels on `stream` (the attention pass and a small merge of
  * sequences split across waves).
  * ---------------------------------------------------------------------- */
-size_t qwen3_paged_decode_workspace_bytes(int B, int num_heads, int head_dim,
-                                          int64_t max_pages, int block_size);
+size_t qwen3_paged_decode_workspace_bytes(int B, int num_heads, int num_kv_heads,
+                                          int head_dim, int64_t max_pages, int block_size);
 
 int qwen3_paged_decode_bf16(const void* q, const int64_t q_strides[2],
                             const void* k_cache, const int64_t k_strides[3],
@@ -231,16 +232,21 @@ int qwen3_kv_write_slots_bf16(const void* k_new, const int64_t k_new_strides[2],
  *             past the first max_seqlen rounded up to the kernel's query
  *             tile are not written; a larger bound only costs empty work
  *             items and gives the same bits.
- *   workspace  optional (NULL: static schedule, no split items):
- *             qwen3_varlen_prefill_workspace_bytes() bytes (about 35 MB) of
- *             device memory, zeroed before its first use; every call leaves
- *             its counters at zero.  With it a batch large enough for
- *             eight-wave workgroups has its work items dealt from counters
- *             as workgroups finish (heaviest first), and a causal batch with
- *             fewer work items than resident workgroups has its heaviest
- *             items cut into two key ranges whose partial states (the last
- *             35 MB) meet in the workspace -- the same bits whichever half
- *             finishes first.  Concurrent calls need separate workspaces.
+ *   workspace  optional (NULL: every item runs whole in one workgroup):
+ *             qwen3_varlen_prefill_workspace_bytes() bytes (69 MB on a
+ *             256-CU device: the size follows the current device's CU
+ *             count) of device memory, zeroed before its first use; every
+ *             call leaves its counters and tickets at zero.  With it a batch
+ *             large enough for eight-wave workgroups has its work items
+ *             dealt from counters as workgroups finish (heaviest first), and
+ *             a batch with fewer work items than resident workgroups is cut
+ *             into equal ranges of key tiles, one per workgroup; an item
+ *             whose tiles span several ranges leaves one partial softmax
+ *             state per range in the workspace and the last part to arrive
+ *             folds them in key order (no part waits for another; the same
+ *             bits whichever part arrives last).  Items of at most four key
+ *             tiles (prompts of at most 256 tokens) are never cut.
+ *             Concurrent calls need separate workspaces.
  * Supported: head_dim 128, num_heads / num_kv_heads in [1, 16].
  * ---------------------------------------------------------------------- */
 size_t qwen3_varlen_prefill_workspace_bytes(void);

@@ -25,7 +25,7 @@ _SIGNATURES = {
     "qwen3_attn_abi_version": (_i, []),
     "qwen3_hbm_read_reference": (_i, [_vp, _i64, _i, _vp, _vp]),
     "qwen3_mfma_rate_reference": (_i, [_i, _vp, _c_i64p, _vp]),
-    "qwen3_paged_decode_workspace_bytes": (ctypes.c_size_t, [_i, _i, _i, _i64, _i]),
+    "qwen3_paged_decode_workspace_bytes": (ctypes.c_size_t, [_i, _i, _i, _i, _i64, _i]),
     "qwen3_paged_decode_bf16": (
         _i,
         [_vp, _c_i64p, _vp, _c_i64p, _vp, _c_i64p, _i64,
@@ -115,7 +115,7 @@ _SIGNATURES = {
     ),
 }
 
-ABI_VERSION = 7
+ABI_VERSION = 8
 
 _lib = None
 

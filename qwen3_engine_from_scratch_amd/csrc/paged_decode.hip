@@ -921,15 +921,21 @@ char* scratch_on(int dev) {
 
 }  // namespace
 
-extern "C" size_t qwen3_paged_decode_workspace_bytes(int B, int num_heads, int head_dim,
-                                                     int64_t max_pages, int block_size) {
-  if (B <= 0 || num_heads <= 0 || head_dim != kD || max_pages <= 0 || block_size <= 0 ||
-      block_size % kTile != 0)
+extern "C" size_t qwen3_paged_decode_workspace_bytes(int B, int num_heads, int num_kv_heads,
+                                                     int head_dim, int64_t max_pages,
+                                                     int block_size) {
+  if (B <= 0 || num_heads <= 0 || num_kv_heads <= 0 || num_heads % num_kv_heads != 0 ||
+      num_heads / num_kv_heads > kMaxG || head_dim != kD || max_pages <= 0 ||
+      block_size <= 0 || block_size % kTile != 0)
     return 0;
-  // Upper bound over every group size and up to kStreamMaxWgs workgroups, so
-  // the size depends only on the launch shape.
-  if (B <= kStreamMaxB)
-    return static_cast<size_t>(stream_layout(B, int64_t(kStreamMaxWgs) * kWaves, kMaxG).total);
+  // Sized for the current device's persistent waves (the largest grid when
+  // no device can be queried) and the shape's group size: it depends only
+  // on the launch shape, never on the live lengths.
+  if (B <= kStreamMaxB) {
+    const int wgs = stream_workgroups();
+    const int64_t waves = int64_t(wgs > 0 ? wgs : kStreamMaxWgs) * kWaves;
+    return static_cast<size_t>(stream_layout(B, waves, num_heads / num_kv_heads).total);
+  }
   return static_cast<size_t>(grid_bytes(B, num_heads, max_pages, block_size));
 }
 
@@ -948,8 +954,8 @@ extern "C" int qwen3_paged_decode_bf16(
                        head_dim, block_size, scale))
     return rc;
   if (B == 0) return QWEN3_OK;
-  const size_t need = qwen3_paged_decode_workspace_bytes(B, num_heads, head_dim, max_pages,
-                                                         block_size);
+  const size_t need = qwen3_paged_decode_workspace_bytes(B, num_heads, num_kv_heads, head_dim,
+                                                         max_pages, block_size);
   if (need == 0) return q3::fail(QWEN3_EINVAL, "%s: cannot size the workspace", who);
   if (!workspace || workspace_bytes < need)
     return q3::fail(QWEN3_EWORKSPACE, "%s: workspace of %zu bytes needed, %zu given", who,

@@ -7,11 +7,11 @@
 // bf16 output.
 //
 // Design (MI355X-first):
-//  * One 256-thread workgroup (4 wave64s) per (query tile, head group,
-//    sequence).  The head group holds HG query heads that share one KV head
-//    (HG = the largest of 4, 2, 1 dividing G), so a K/V tile staged in LDS
-//    serves every head of the group; each wave owns 32 query rows of one
-//    head.  Two workgroups share a CU (two waves per SIMD), so one wave's
+//  * A work item is (query tile, head group, sequence).  The head group
+//    holds HG query heads that share one KV head (HG = the largest of 4, 2,
+//    1 dividing G), so a K/V tile staged in LDS serves every head of the
+//    group; each wave of a workgroup owns 32 query rows of one head.  Two
+//    256-thread workgroups share a CU (two waves per SIMD), so one wave's
 //    softmax overlaps the other's matrix-core work.
 //  * K/V tiles of 64 keys go from HBM straight into LDS with buffer loads
 //    that write LDS (no staging registers), double-buffered: the next tile's
@@ -32,6 +32,14 @@
 //    running max is only raised (and the accumulator rescaled) when a new
 //    score exceeds it by more than 2^8, which keeps every P <= 256 and makes
 //    rescales rare; masking runs only on diagonal and tail tiles.
+//  * Range schedule (varlen_prefill_range_kernel): the items' key tiles,
+//    each weighted by its cost plus a fixed cost per item, are laid end to
+//    end and cut into equal ranges, one per resident workgroup.  A
+//    workgroup streams its range as a chain of segments (runs of one
+//    item's key tiles): the next segment's first K/V tile and Q rows load
+//    during the current segment's last tile.  An item whose tiles fall in
+//    several ranges leaves one partial softmax state per range in the
+//    workspace; the last part to arrive folds them in key order.
 #include "common.hpp"
 
 namespace {
@@ -47,13 +55,28 @@ template <int W>
 constexpr int dma_per_wave() { return kBN * kRowBytes / (W * 64 * 16); }  // 16-byte lanes
 constexpr int kMaxDma = 4;
 constexpr float kRescaleSlack = 8.f;      // log2 headroom before the max is raised
-constexpr int kMaxSeqs = 256;             // persistent path: sequences ranked in LDS
+constexpr int kMaxSeqs = 256;             // persistent / range paths: sequences ranked in LDS
 constexpr int kScanMax = 1024;            // persistent path: query-tile ranks in LDS
 constexpr int kPools = 8;                 // dynamic schedule: one item pool per XCD
 constexpr int kPoolStride = 32;           // counters 128 bytes apart
-constexpr int kMaxSplits = 256;           // work items cut in two per call, at most
-constexpr int kSplitSlotFloats = 8 * 64 * 66;  // eight waves x 64 lanes x (64 sums, max, sum)
 static_assert(dma_per_wave<4>() == kMaxDma && dma_per_wave<8>() == 2, "tile / workgroup shape");
+
+// Range schedule weights: a key tile is kUnits, an item adds kItemUnits,
+// its start and output (measured per-workgroup timelines: about 2.5 tiles'
+// time from one item's last tile to the next item's first).  Items of at
+// most kAtomicTiles key tiles are never cut (so a prompt of at most 256
+// tokens is computed the same way in any batch); a range holds at least
+// kMinRangeTiles tiles' weight.
+constexpr int kUnits = 16;
+constexpr int kItemUnits = 40;
+constexpr int kAtomicTiles = 4;
+constexpr int kMinRangeTiles = 4;
+// Partial softmax state of one workgroup in the workspace: per wave and
+// lane 64 accumulators (16 float4 rows), then (running max, sum share).
+template <int W>
+constexpr int slot_floats() { return W * 64 * 66; }
+template <int W>
+constexpr int slot_ml_offset() { return W * 64 * 64 * 4; }  // bytes before the (max, sum) pairs
 
 typedef __attribute__((address_space(3))) void lds_void_t;
 typedef short i16x4 __attribute__((__vector_size__(4 * sizeof(short))));
@@ -78,10 +101,12 @@ struct PrefillArgs {
   float scale_log2;
   int causal;
   uint32_t* ctr;  // nullable: [32 p] next item of pool p, [32 kPools] workgroups done (zero between calls)
-  // Split work items (split kernel only): per slot a ticket and a ready
-  // flag (zero between calls) and the first finisher's partial state.
-  uint32_t* split_ctr;  // [kMaxSplits][2]
-  float* split_buf;     // [kMaxSplits][kSplitSlotFloats]
+  // Range path: per range that holds the first tile of a cut item, the
+  // number of its parts that have arrived (zero between calls), and two
+  // partial-state slots per range (its first and its last segment).
+  uint32_t* tickets;  // [max_ranges]
+  float* slots;       // [2 * max_ranges][slot_floats<W>()]
+  int max_ranges;
 };
 
 // The staged tiles of one workgroup: two K and two V buffers.
@@ -173,7 +198,7 @@ __device__ __forceinline__ q3::bf16x8 lds_vt(const uint16_t* base, uint32_t byte
 }
 
 // LDS operand distance of the MFMA loops (steps read ahead).
-constexpr int kAhead = 4;
+constexpr int kAhead = 2;
 
 // Byte offset of the K operand of QK step u (key block u % 2, d step u / 2).
 __device__ __forceinline__ uint32_t qk_operand(const LaneOffsets& off, int u) {
@@ -236,294 +261,179 @@ __device__ __forceinline__ void wait_loads() {
   __builtin_amdgcn_s_waitcnt(0x0f70);
 }
 
-// Partial state of one wave of a split item, in its slot: accumulators as
-// 16 float4 rows of 64 lanes, then (max, sum share) per lane.  Written and
-// read with device-scope accesses (sc1: written through to, and read from,
-// the point where all XCDs' L2s agree), so the hand-off needs no L2
-// write-back or invalidation, which would stall the whole XCD.
-constexpr int kCpolDevice = 16;  // sc1
-constexpr int kSlotMlOffset = 8 * 64 * 64 * 4;  // bytes before the (max, sum) pairs
+// One wave's share of a work item: the sequence's rows, this wave's 32
+// query rows of one head (wave-uniform).
+struct WaveItem {
+  int64_t start;  // first row of the sequence
+  int len;        // its length
+  int head;       // query head of this wave
+  int kvh;        // its KV head
+  int q0;         // first query row of this wave (lane l owns row q0 + l % 32)
+  __device__ __forceinline__ bool active() const { return q0 < len; }
+  __device__ __forceinline__ int last_q() const { return min(q0 + 31, len - 1); }
+};
 
-__device__ __forceinline__ __amdgpu_buffer_rsrc_t slot_rsrc(float* slot) {
-  return __builtin_amdgcn_make_buffer_rsrc(slot, 0, kSplitSlotFloats * 4, 0x00020000);
-}
-
-__device__ __forceinline__ void save_partial(__amdgpu_buffer_rsrc_t slot, int wave, int lane,
-                                             float m_run, float l_run, const q3::f32x16 (&acc)[4]) {
-#pragma unroll
-  for (int db = 0; db < 4; ++db)
-#pragma unroll
-    for (int r4 = 0; r4 < 4; ++r4) {
-      const q3::f32x4 v = {acc[db][4 * r4], acc[db][4 * r4 + 1], acc[db][4 * r4 + 2],
-                           acc[db][4 * r4 + 3]};
-      __builtin_amdgcn_raw_buffer_store_b128(
-          __builtin_bit_cast(q3::u32x4, v), slot,
-          static_cast<uint32_t>(((wave * 16 + db * 4 + r4) * 64 + lane) * 16), 0, kCpolDevice);
-    }
-  const uint32_t ml = kSlotMlOffset + (wave * 64 + lane) * 8;
-  __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(m_run), slot, ml, 0, kCpolDevice);
-  __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(l_run), slot, ml + 4, 0, kCpolDevice);
-}
-
-// Folds the other part's saved state into (m_run, l_run, acc) (both
-// relative to their own running max; the result is relative to the larger
-// one).  The sums are
-// formed as part 0 * its weight + part 1 * its weight whichever part merges,
-// so the output does not depend on which part finished first.
-__device__ __forceinline__ void merge_partial(__amdgpu_buffer_rsrc_t slot, int wave, int lane,
-                                              bool own_first, float& m_run, float& l_run,
-                                              q3::f32x16 (&acc)[4]) {
-  // Every load in flight at once: one memory round trip.
-  const uint32_t ml = kSlotMlOffset + (wave * 64 + lane) * 8;
-  const float om = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(slot, ml, 0, kCpolDevice));
-  const float ol =
-      __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(slot, ml + 4, 0, kCpolDevice));
-  q3::f32x4 v[16];
-#pragma unroll
-  for (int i = 0; i < 16; ++i)
-    v[i] = __builtin_bit_cast(
-        q3::f32x4, __builtin_amdgcn_raw_buffer_load_b128(
-                       slot, static_cast<uint32_t>(((wave * 16 + i) * 64 + lane) * 16), 0,
-                       kCpolDevice));
-  __builtin_amdgcn_sched_barrier(0);
-  const float m = fmaxf(m_run, om);
-  if (m == q3::kNegInf) return;  // no key reached this row in either part
-  const float a_own = q3::fast_exp2(m_run - m);  // exp2(-inf) = 0
-  const float a_oth = q3::fast_exp2(om - m);
-  const float w0 = own_first ? a_own : a_oth, w1 = own_first ? a_oth : a_own;
-  m_run = m;
-  {
-    const float x0 = own_first ? l_run : ol, x1 = own_first ? ol : l_run;
-    l_run = __builtin_fmaf(x1, w1, x0 * w0);
-  }
-#pragma unroll
-  for (int i = 0; i < 16; ++i)
-#pragma unroll
-    for (int e = 0; e < 4; ++e) {
-      const float own = acc[i >> 2][4 * (i & 3) + e];
-      const float x0 = own_first ? own : v[i][e], x1 = own_first ? v[i][e] : own;
-      acc[i >> 2][4 * (i & 3) + e] = __builtin_fmaf(x1, w1, x0 * w0);
-    }
-}
-
-// One work item: query tile mt of sequence seq for head group hg, over all
-// of its key tiles (part < 0) or, in the split kernel, over the first
-// (part 0) or second (part 1) half of them.  The two parts of a split item
-// meet through split slot `slot`: the first to finish saves its partial
-// state and raises the slot's ready flag; the second waits for that flag
-// (the first is past all its work by then, so the wait is short), merges
-// and writes the output, then leaves the slot's ticket and flag at zero.
-// Every thread of the workgroup calls it.
-template <int W, bool Split = false>
-__device__ __forceinline__ void prefill_item(const PrefillArgs& a, const LaneOffsets& off,
-                                             int64_t start, int len, int hg, int mt,
-                                             const TileBufs& tb, int part = -1, int slot = 0,
-                                             uint32_t* s_role = nullptr) {
-  const int m0 = mt * a.rows;
-  if (m0 >= len) return;
-
-  const int tid = threadIdx.x;
-  const int lane = tid & 63;
-  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // uniform: scalar branches
-  const int l32 = lane & 31;
-  const int hl = lane >> 5;
+template <int W>
+__device__ __forceinline__ WaveItem wave_item(const PrefillArgs& a, int64_t start, int len, int hg,
+                                              int mt, int wave, int lane) {
+  WaveItem wi;
   const int wph = W / a.HG;  // waves per head
-  const int head = hg * a.HG + wave / wph;
-  const int kvh = (hg * a.HG) / a.G;
-  const int q0 = m0 + (wave % wph) * 32;  // first query row of this wave
-  const int qrow = q0 + l32;               // the query column this lane owns
+  wi.start = start;
+  wi.len = len;
+  wi.head = hg * a.HG + wave / wph;
+  wi.kvh = (hg * a.HG) / a.G;
+  wi.q0 = mt * a.rows + (wave % wph) * 32;
+  return wi;
+}
 
-  const int kend = a.causal ? min(len, m0 + a.rows) : len;
-  const int n_tiles = (kend + kBN - 1) / kBN;
-  const int t0 = Split && part == 1 ? n_tiles / 2 : 0;
-  const int t1 = Split && part == 0 ? n_tiles / 2 : n_tiles;
-
-  tile_dma<W>(a, off, start, len, kvh, t0 * kBN, tb.k0, tb.v0, wave);
-
-  // Q^T as the B operand: lane (query l32, k-group hl), chunk c: dims
-  // c*16 + 8*hl .. +7.
-  q3::bf16x8 qv[8];
-  {
-    const q3::u32x4 z = {0u, 0u, 0u, 0u};
-    const bool ok = qrow < len;
-    const uint16_t* qp =
-        a.q + (start + (ok ? qrow : 0)) * a.q_st + static_cast<int64_t>(head) * a.q_sh + 8 * hl;
+// Q^T as the B operand: lane (query l32, k-group hl), chunk c: dims
+// c*16 + 8*hl .. +7.  The wave's 32 rows are read through a buffer
+// descriptor that ends at the sequence's last row, so rows past it read as
+// zero; q_lane is the lane's byte offset l32 * row stride + 16 hl, the
+// same for every item.  The chunk offset c * 32 goes in the scalar offset,
+// which the range check does not cover: the lane's row start (in the
+// vector offset) decides, and a row in range is in range up to its end.
+__device__ __forceinline__ uint32_t q_lane_offset(const PrefillArgs& a, int lane) {
+  return static_cast<uint32_t>((lane & 31) * a.q_st * 2 + 16 * (lane >> 5));
+}
+__device__ __forceinline__ void load_q(const PrefillArgs& a, const WaveItem& wi, uint32_t q_lane,
+                                       q3::bf16x8 (&qv)[8]) {
+  const int rows = min(32, wi.len - wi.q0);
+  const uint16_t* base =
+      a.q + (wi.start + wi.q0) * a.q_st + static_cast<int64_t>(wi.head) * a.q_sh;
+  const int bytes = rows > 0 ? static_cast<int>((rows - 1) * a.q_st * 2) + kRowBytes : 0;
+  const __amdgpu_buffer_rsrc_t qr =
+      __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t*>(base), 0, bytes, 0x00020000);
 #pragma unroll
-    for (int c = 0; c < 8; ++c) qv[c] = q3::as_bf16x8(ok ? q3::ld16(qp + c * 16) : z);
-  }
+  for (int c = 0; c < 8; ++c)
+    qv[c] = q3::as_bf16x8(__builtin_bit_cast(
+        q3::u32x4, __builtin_amdgcn_raw_buffer_load_b128(qr, q_lane, c * 32, 0)));
+}
 
-  float m_run = q3::kNegInf;  // running max (log2 domain) of this query
-  float l_run = 0.f;          // this lane's share of the denominator
-  q3::f32x16 acc[4];          // acc[db][r] = O[qrow][32*db + 8*(r/4) + 4*hl + r%4]
-#pragma unroll
-  for (int db = 0; db < 4; ++db)
-#pragma unroll
-    for (int r = 0; r < 16; ++r) acc[db][r] = 0.f;
-
-  const bool wave_active = q0 < len;
-  const int wave_last_q = min(q0 + 31, len - 1);
+// One 64-key tile (first key n0, staged in kt / vt) folded into this wave's
+// online softmax state.
+__device__ __forceinline__ void tile_math(const PrefillArgs& a, const LaneOffsets& off,
+                                          const WaveItem& wi, int lane, int n0,
+                                          const uint16_t* kt, const uint16_t* vt,
+                                          const q3::bf16x8 (&qv)[8], float& m_run, float& l_run,
+                                          q3::f32x16 (&acc)[4]) {
+  const int hl = lane >> 5;
   const float c = a.scale_log2;
-
-  wait_loads();
-  __syncthreads();
-
-  auto tile = [&](int it, const uint16_t* kt, const uint16_t* vt, uint16_t* nk, uint16_t* nv) {
-    const int n0 = it * kBN;
-    if (it + 1 < t1) tile_dma<W>(a, off, start, len, kvh, n0 + kBN, nk, nv, wave);
-
-    // Causal: the tile is entirely above this wave's last query row.
-    const bool wave_skip = !wave_active || (a.causal && n0 > wave_last_q);
-    if (!wave_skip) {
-      // ---- S^T = K Q^T for two 32-key blocks ----
-      // Step u covers key block u % 2, dims 16 (u / 2) .. +15; the two
-      // blocks' chains alternate and K operands are read 4 steps ahead (the
-      // scheduling fences keep that distance).
-      q3::f32x16 s[2];
+  // Causal: the tile is entirely above this wave's last query row.
+  const bool wave_skip = !wi.active() || (a.causal && n0 > wi.last_q());
+  if (wave_skip) return;
+  // ---- S^T = K Q^T for two 32-key blocks ----
+  // Step u covers key block u % 2, dims 16 (u / 2) .. +15; the two blocks'
+  // chains alternate and K operands are read 4 steps ahead (the scheduling
+  // fences keep that distance).
+  q3::f32x16 s[2];
 #pragma unroll
-      for (int kb = 0; kb < 2; ++kb)
+  for (int kb = 0; kb < 2; ++kb)
 #pragma unroll
-        for (int r = 0; r < 16; ++r) s[kb][r] = 0.f;
-      {
-        q3::bf16x8 kf[kAhead];
+    for (int r = 0; r < 16; ++r) s[kb][r] = 0.f;
+  {
+    q3::bf16x8 kf[kAhead];
 #pragma unroll
-        for (int u = 0; u < kAhead; ++u) kf[u] = lds_ld16(kt, qk_operand(off, u));
-        __builtin_amdgcn_sched_barrier(0);
+    for (int u = 0; u < kAhead; ++u) kf[u] = lds_ld16(kt, qk_operand(off, u));
+    __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-        for (int u = 0; u < 16; ++u) {
-          s[u & 1] = q3::mfma32x32x16(kf[u % kAhead], qv[u >> 1], s[u & 1]);
-          if (u + kAhead < 16) kf[u % kAhead] = lds_ld16(kt, qk_operand(off, u + kAhead));
-          __builtin_amdgcn_sched_barrier(0);
-        }
-      }
-      // ---- mask (diagonal / tail tiles only) and block max ----
-      const bool need_mask = (n0 + kBN > len) || (a.causal && n0 + kBN - 1 > q0);
-      if (need_mask) {
-        // score (kb, r) is key n0 + 4 hl + kr with kr = 32 kb + 8 (r / 4) +
-        // r % 4 (an inline constant): compare kr with per-lane limits
-        const int lim_len = len - n0 - 4 * hl;                   // kr < lim_len
-        const int lim_q = a.causal ? qrow - n0 - 4 * hl : kBN;  // kr <= lim_q
-#pragma unroll
-        for (int kb = 0; kb < 2; ++kb)
-#pragma unroll
-          for (int r = 0; r < 16; ++r) {
-            const int kr = kb * 32 + 8 * (r / 4) + (r % 4);
-            const bool valid = kr < lim_len && kr <= lim_q;
-            s[kb][r] = valid ? s[kb][r] : q3::kNegInf;
-          }
-      }
-      // Row max as a v_max3 chain over the lane's 32 scores.  Written as asm
-      // because fmaxf would first canonicalize every MFMA result (one more
-      // VALU op per score); a NaN score makes P, and so the output, NaN
-      // either way.  The scores were written by the QK MFMAs just above:
-      // 24 wait states cover the MFMA-to-VALU dependency.
-      asm volatile("s_nop 7\n\ts_nop 7\n\ts_nop 7");
-      float bm = max3_scores(s);
-      bm = cross_half_max(bm);
-      const float m_cand = bm * c;
-      const bool raise = m_cand > m_run + kRescaleSlack;
-      if (__any(raise)) {
-        const float m_new = raise ? m_cand : m_run;
-        const float alpha = raise ? q3::fast_exp2(m_run - m_new) : 1.f;
-        m_run = m_new;
-        l_run *= alpha;
-#pragma unroll
-        for (int db = 0; db < 4; ++db) acc[db] *= alpha;
-      }
-      // V^T operands of the first PV steps are read before the exponentials,
-      // which hide their latency.
-      q3::bf16x8 vf[kAhead];
-#pragma unroll
-      for (int u = 0; u < kAhead; ++u) vf[u] = lds_vt(vt, pv_operand(off, u));
+    for (int u = 0; u < 16; ++u) {
+      s[u & 1] = q3::mfma32x32x16(kf[u % kAhead], qv[u >> 1], s[u & 1]);
+      if (u + kAhead < 16) kf[u % kAhead] = lds_ld16(kt, qk_operand(off, u + kAhead));
       __builtin_amdgcn_sched_barrier(0);
-      const float m_use = m_run == q3::kNegInf ? 0.f : m_run;
-      // ---- P = exp2(s * c - m) as P^T B operands (chunk g = 2 kb + kc:
-      // scores s[kb][8 kc .. 8 kc + 7]) and O^T += V^T P^T, step u covering
-      // key chunk u / 4, dims 32 (u % 4) .. +31.  Chunk 0 is computed
-      // first; the exponentials of chunk g + 1 are issued between the four
-      // MFMAs of chunk g, two per step, so the VALU works while the matrix
-      // core runs.
-      q3::u32x4 pk[4];
-      float psum[4];  // four independent sum chains, started by chunk 0
-      auto exp_pair = [&](int g, int h) {  // scores 2h, 2h + 1 of chunk g
-        const int kb = g >> 1, kc = g & 1;
-        const float e0 = q3::fast_exp2(__builtin_fmaf(s[kb][8 * kc + 2 * h], c, -m_use));
-        const float e1 = q3::fast_exp2(__builtin_fmaf(s[kb][8 * kc + 2 * h + 1], c, -m_use));
-        if (g == 0 && h < 2) {
-          psum[2 * h] = e0;
-          psum[2 * h + 1] = e1;
-        } else {
-          psum[(2 * h) & 3] += e0;
-          psum[(2 * h + 1) & 3] += e1;
-        }
-        pk[g][h] = q3::pack_bf16x2(e0, e1);
-      };
-#pragma unroll
-      for (int h = 0; h < 4; ++h) exp_pair(0, h);
-      __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-      for (int u = 0; u < 16; ++u) {
-        acc[u & 3] = q3::mfma32x32x16(vf[u % kAhead], q3::as_bf16x8(pk[u >> 2]), acc[u & 3]);
-        if (u + kAhead < 16) vf[u % kAhead] = lds_vt(vt, pv_operand(off, u + kAhead));
-        if (u < 12) exp_pair((u >> 2) + 1, u & 3);
-        __builtin_amdgcn_sched_barrier(0);
-      }
-      l_run += (psum[0] + psum[1]) + (psum[2] + psum[3]);
     }
-    wait_loads();
-    __syncthreads();
+  }
+  // ---- mask (diagonal / tail tiles only) and block max ----
+  const bool need_mask = (n0 + kBN > wi.len) || (a.causal && n0 + kBN - 1 > wi.q0);
+  if (need_mask) {
+    // score (kb, r) is key n0 + 4 hl + kr with kr = 32 kb + 8 (r / 4) + r %
+    // 4 (an inline constant): valid iff kr <= lim, one per-lane limit for
+    // the sequence end and the causal diagonal.
+    int lim = wi.len - 1 - n0 - 4 * hl;
+    if (a.causal) lim = min(lim, wi.q0 + (lane & 31) - n0 - 4 * hl);
+#pragma unroll
+    for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int kr = kb * 32 + 8 * (r / 4) + (r % 4);
+        s[kb][r] = kr <= lim ? s[kb][r] : q3::kNegInf;
+      }
+  }
+  // Row max as a v_max3 chain over the lane's 32 scores.  The scores were
+  // written by the QK MFMAs just above: 24 wait states cover the
+  // MFMA-to-VALU dependency.
+  asm volatile("s_nop 7\n\ts_nop 7\n\ts_nop 7");
+  float bm = max3_scores(s);
+  bm = cross_half_max(bm);
+  const float m_cand = bm * c;
+  const bool raise = m_cand > m_run + kRescaleSlack;
+  if (__any(raise)) {
+    const float m_new = raise ? m_cand : m_run;
+    const float alpha = raise ? q3::fast_exp2(m_run - m_new) : 1.f;
+    m_run = m_new;
+    l_run *= alpha;
+#pragma unroll
+    for (int db = 0; db < 4; ++db) acc[db] *= alpha;
+  }
+  // V^T operands of the first PV steps are read before the exponentials,
+  // which hide their latency.
+  q3::bf16x8 vf[kAhead];
+#pragma unroll
+  for (int u = 0; u < kAhead; ++u) vf[u] = lds_vt(vt, pv_operand(off, u));
+  __builtin_amdgcn_sched_barrier(0);
+  const float m_use = m_run == q3::kNegInf ? 0.f : m_run;
+  // ---- P = exp2(s * c - m) as P^T B operands (chunk g = 2 kb + kc:
+  // scores s[kb][8 kc .. 8 kc + 7]) and O^T += V^T P^T, step u covering
+  // key chunk u / 4, dims 32 (u % 4) .. +31.  Chunk 0 is computed first;
+  // the exponentials of chunk g + 1 are issued between the four MFMAs of
+  // chunk g, two per step, so the VALU works while the matrix core runs.
+  q3::u32x4 pk[4];
+  float psum[4];  // four independent sum chains, started by chunk 0
+  auto exp_pair = [&](int g, int h) {  // scores 2h, 2h + 1 of chunk g
+    const int kb = g >> 1, kc = g & 1;
+    const float e0 = q3::fast_exp2(__builtin_fmaf(s[kb][8 * kc + 2 * h], c, -m_use));
+    const float e1 = q3::fast_exp2(__builtin_fmaf(s[kb][8 * kc + 2 * h + 1], c, -m_use));
+    if (g == 0 && h < 2) {
+      psum[2 * h] = e0;
+      psum[2 * h + 1] = e1;
+    } else {
+      psum[(2 * h) & 3] += e0;
+      psum[(2 * h + 1) & 3] += e1;
+    }
+    pk[g][h] = q3::pack_bf16x2(e0, e1);
   };
-
-  for (int it = t0; it < t1; it += 2) {
-    tile(it, tb.k0, tb.v0, tb.k1, tb.v1);
-    if (it + 1 < t1) tile(it + 1, tb.k1, tb.v1, tb.k0, tb.v0);
+#pragma unroll
+  for (int h = 0; h < 4; ++h) exp_pair(0, h);
+  __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+  for (int u = 0; u < 16; ++u) {
+    acc[u & 3] = q3::mfma32x32x16(vf[u % kAhead], q3::as_bf16x8(pk[u >> 2]), acc[u & 3]);
+    if (u + kAhead < 16) vf[u % kAhead] = lds_vt(vt, pv_operand(off, u + kAhead));
+    if (u < 12) exp_pair((u >> 2) + 1, u & 3);
+    __builtin_amdgcn_sched_barrier(0);
   }
+  l_run += (psum[0] + psum[1]) + (psum[2] + psum[3]);
+}
 
-  if constexpr (Split) {
-    if (part >= 0) {
-      uint32_t* ticket = a.split_ctr + 2 * slot;
-      uint32_t* ready = ticket + 1;
-      const __amdgpu_buffer_rsrc_t saved =
-          slot_rsrc(a.split_buf + static_cast<int64_t>(slot) * kSplitSlotFloats);
-      if (tid == 0)
-        *s_role = __hip_atomic_fetch_add(ticket, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      __syncthreads();
-      if (*s_role == 0) {
-        save_partial(saved, wave, lane, m_run, l_run, acc);
-        wait_loads();  // this wave's device-scope saves are complete
-        __syncthreads();
-        if (tid == 0) __hip_atomic_store(ready, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        return;
-      }
-      if (tid == 0) {
-        // Bounded: with the ticket taken, the other part only has its
-        // saves left.  (A workspace not zeroed before its first call could
-        // leave the flag down; the cap ends the wait all the same.)
-        for (int spin = 0; spin < (1 << 22); ++spin) {
-          if (__hip_atomic_load(ready, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) != 0u) break;
-          __builtin_amdgcn_s_sleep(1);
-        }
-      }
-      __syncthreads();  // the saves are read (device scope) only after the flag
-      merge_partial(saved, wave, lane, part == 0, m_run, l_run, acc);
-      if (tid == 0) {
-        __hip_atomic_store(ticket, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        __hip_atomic_store(ready, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      }
-    }
-  }
+// Byte offset of this lane's 16-byte output chunk in the first of the four
+// rows one store instruction writes (lane / 16 selects the row, lane % 16
+// the chunk), the same for every item.
+__device__ __forceinline__ uint32_t o_lane_offset(const PrefillArgs& a, int lane) {
+  return static_cast<uint32_t>((lane >> 4) * a.o_st * 2 + 16 * (lane & 15));
+}
 
-  l_run = cross_half_sum(l_run);
-  if (!wave_active) return;
-  // The output goes through LDS so that each global store writes whole
-  // 256-byte rows (four per instruction) instead of 16 bytes of 32 rows:
-  // every tile buffer is free after the loop's last barrier, and the
-  // caller's barrier follows before the next item's loads refill them.
-  // Wave w stages its 32 x 128 tile in 8 KiB of buffer w / 2, chunk c of
-  // row r at chunk c ^ (r % 16) (conflict-free for both directions).
-  const float inv = l_run > 0.f ? 1.f / l_run : 0.f;  // 0 for rows past the end
-  const int sb = wave >> 1;
-  char* stage = reinterpret_cast<char*>(sb == 0 ? tb.k0 : sb == 1 ? tb.v0 : sb == 2 ? tb.k1 : tb.v1) +
-                (wave & 1) * 8192;
+// Normalises this wave's 32 x 128 output tile (l: the row's full sum) and
+// writes its valid rows.  The tile goes through 8 KiB of LDS at `stage`
+// (chunk c of row r at chunk c ^ (r % 16), conflict-free both ways) so
+// that each store writes four whole 256-byte rows; the stores go through a
+// buffer descriptor that ends at the sequence's last row, so rows past it
+// are dropped without a branch.  The caller's barrier must follow before
+// `stage` is written again.
+__device__ __forceinline__ void store_output(const PrefillArgs& a, const WaveItem& wi, int lane,
+                                             uint32_t o_lane, float l,
+                                             const q3::f32x16 (&acc)[4], char* stage) {
+  const int l32 = lane & 31, hl = lane >> 5;
+  const float inv = l > 0.f ? 1.f / l : 0.f;  // 0 for rows past the end
 #pragma unroll
   for (int db = 0; db < 4; ++db)
 #pragma unroll
@@ -533,16 +443,86 @@ __device__ __forceinline__ void prefill_item(const PrefillArgs& a, const LaneOff
                      q3::pack_bf16x2(acc[db][4 * g4 + 2] * inv, acc[db][4 * g4 + 3] * inv)};
       *reinterpret_cast<q3::u32x2*>(stage + l32 * 256 + ((ch ^ (l32 & 15)) << 4) + hl * 8) = w;
     }
+  const int rows = min(32, wi.len - wi.q0);
+  uint16_t* base = a.o + (wi.start + wi.q0) * a.o_st + static_cast<int64_t>(wi.head) * a.o_sh;
+  const int bytes = rows > 0 ? static_cast<int>((rows - 1) * a.o_st * 2) + kRowBytes : 0;
+  const __amdgpu_buffer_rsrc_t orr = __builtin_amdgcn_make_buffer_rsrc(base, 0, bytes, 0x00020000);
   const int oc = lane & 15;  // this lane's 16-byte chunk of a row
 #pragma unroll
   for (int j = 0; j < 8; ++j) {
     const int rr = 4 * j + (lane >> 4);
     const q3::u32x4 v =
         *reinterpret_cast<const q3::u32x4*>(stage + rr * 256 + ((oc ^ (rr & 15)) << 4));
-    const int row = q0 + rr;
-    if (row < len)
-      q3::st16(a.o + (start + row) * a.o_st + static_cast<int64_t>(head) * a.o_sh + oc * 8, v);
+    // the row offset in the vector offset: the range check covers it (it
+    // does not cover the scalar offset)
+    __builtin_amdgcn_raw_buffer_store_b128(
+        v, orr, o_lane + static_cast<uint32_t>(4 * j * a.o_st * 2), 0, 0);
   }
+}
+
+// ---------------------------------------------------------------------------
+// Whole items (flat and persistent grids).
+
+// Key tiles [t0, t1) of one work item folded into a fresh online softmax
+// state (m_run, l_run, acc): the first tile and the Q rows load, then each
+// tile's loads are issued before the previous tile's math (two buffer
+// pairs, one barrier per tile).  Every thread of the workgroup calls it;
+// all four tile buffers are free when it returns.
+template <int W>
+__device__ __forceinline__ void run_tiles(const PrefillArgs& a, const LaneOffsets& off,
+                                          const WaveItem& wi, int t0, int t1, const TileBufs& tb,
+                                          int lane, int wave, float& m_run, float& l_run,
+                                          q3::f32x16 (&acc)[4]) {
+  tile_dma<W>(a, off, wi.start, wi.len, wi.kvh, t0 * kBN, tb.k0, tb.v0, wave);
+  q3::bf16x8 qv[8];
+  load_q(a, wi, q_lane_offset(a, lane), qv);
+  m_run = q3::kNegInf;  // running max (log2 domain) of this query
+  l_run = 0.f;          // this lane's share of the denominator
+#pragma unroll
+  for (int db = 0; db < 4; ++db)
+#pragma unroll
+    for (int r = 0; r < 16; ++r) acc[db][r] = 0.f;
+  wait_loads();
+  __syncthreads();
+  auto tile = [&](int it, const uint16_t* kt, const uint16_t* vt, uint16_t* nk, uint16_t* nv) {
+    if (it + 1 < t1) tile_dma<W>(a, off, wi.start, wi.len, wi.kvh, (it + 1) * kBN, nk, nv, wave);
+    tile_math(a, off, wi, lane, it * kBN, kt, vt, qv, m_run, l_run, acc);
+    wait_loads();
+    __syncthreads();
+  };
+  for (int it = t0; it < t1; it += 2) {
+    tile(it, tb.k0, tb.v0, tb.k1, tb.v1);
+    if (it + 1 < t1) tile(it + 1, tb.k1, tb.v1, tb.k0, tb.v0);
+  }
+}
+
+// This wave's 8 KiB output staging area: wave w in half w % 2 of buffer
+// w / 2 (the tile buffers are free after run_tiles).
+__device__ __forceinline__ char* stage_of(const TileBufs& tb, int wave) {
+  const int sb = wave >> 1;
+  return reinterpret_cast<char*>(sb == 0 ? tb.k0 : sb == 1 ? tb.v0 : sb == 2 ? tb.k1 : tb.v1) +
+         (wave & 1) * 8192;
+}
+
+// One work item: query tile mt of sequence seq for head group hg, over all
+// of its key tiles.  Every thread of the workgroup calls it; the caller's
+// barrier must follow before the tile buffers are loaded again.
+template <int W>
+__device__ __forceinline__ void prefill_item(const PrefillArgs& a, const LaneOffsets& off,
+                                             int64_t start, int len, int hg, int mt,
+                                             const TileBufs& tb) {
+  if (mt * a.rows >= len) return;
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // uniform: scalar branches
+  const WaveItem wi = wave_item<W>(a, start, len, hg, mt, wave, lane);
+  const int kend = a.causal ? min(len, mt * a.rows + a.rows) : len;
+  float m_run, l_run;
+  q3::f32x16 acc[4];  // acc[db][r] = O[q0 + l32][32*db + 8*(r/4) + 4*hl + r%4]
+  run_tiles<W>(a, off, wi, 0, (kend + kBN - 1) / kBN, tb, lane, wave, m_run, l_run, acc);
+  l_run = cross_half_sum(l_run);
+  if (!wi.active()) return;
+  store_output(a, wi, lane, o_lane_offset(a, lane), l_run, acc, stage_of(tb, wave));
 }
 
 // The four staged tile buffers, as separate LDS arrays so loads into one
@@ -688,12 +668,8 @@ __device__ __forceinline__ void item_at(const PrefillArgs& a, int64_t i64, const
 // one runs, and take what other pools have left once theirs is empty.
 // Without them they take their share in a snake order over rounds
 // (mirroring whole groups of 8 positions so item i stays on XCD i % 8).
-#ifndef Q3_PREFILL_PERSISTENT_WAVES_PER_EU
-#define Q3_PREFILL_PERSISTENT_WAVES_PER_EU 2
-#endif
 template <int W>
-__global__ __launch_bounds__(W * 64)
-__attribute__((amdgpu_waves_per_eu(Q3_PREFILL_PERSISTENT_WAVES_PER_EU, Q3_PREFILL_PERSISTENT_WAVES_PER_EU)))
+__global__ __launch_bounds__(W * 64) __attribute__((amdgpu_waves_per_eu(2, 2)))
 void varlen_prefill_persistent_kernel(PrefillArgs a) {
   Q3_PREFILL_TILE_BUFFERS;
   __shared__ int s_len[kMaxSeqs];
@@ -795,151 +771,433 @@ void varlen_prefill_persistent_kernel(PrefillArgs a) {
   }
 }
 
-// Sizes the items for W waves and launches the persistent grid (CUs x
-// resident workgroups, from the occupancy API) or, past its LDS tables, the
-// flat grid.
-// Split plan of a causal batch (with split slots in the workspace).  An
-// item's work is its key tiles, about (mt + 1) rows / 64 for query tile mt,
-// so the heaviest items are those of the highest query tiles -- the first
-// ranks of the list.  The items of query tiles mt >= ms are cut in two at
-// their middle key tile, ms being the lowest query tile whose items are
-// heavier than the batch's mean work per workgroup (and have at least four
-// key tiles, and fit the slots); a split item's slot is its list index.
-// Entries are then ordered by work in half-tile classes: class k holds the
-// whole items of query tile k / 2 - 1 (k even, below ms) followed by the
-// two parts of each item of query tile k - 1 (at or above ms), classes
-// heaviest first.  s_cls[j] = entries before class 2 n_mtiles - j.
-struct SplitPlan {
-  int ms;  // first split query tile (n_mtiles: none)
-  int E;   // work entries
-  int T;   // items
+// ---------------------------------------------------------------------------
+// Range schedule.
+//
+// Items are ordered head group first (so with a multiple of 8 groups each
+// XCD's contiguous share of the ranges reads one KV head's tiles from its
+// L2), then sequences longest first, then query tiles in order.  Item
+// (hg, rank r, mt) sits at weight position hg H + pos[r] + f_r(mt), where
+// f(mt) = kUnits (key tiles of query tiles < mt) + kItemUnits mt, and its
+// tile j's midpoint at that + kItemUnits + kUnits j + kUnits / 2.  Range v
+// of N owns the positions p with floor(p N / U) = v (U: the total weight).
+// A tile belongs to the range holding its midpoint; an item of at most
+// kAtomicTiles tiles goes whole to the range holding its own midpoint.
+
+// Key tiles of query tile mt.
+__device__ __forceinline__ int item_tiles(int len, int mt, int rows, int causal) {
+  const int kend = causal ? min(len, (mt + 1) * rows) : len;
+  return (kend + kBN - 1) / kBN;
+}
+// Key tiles of query tiles 0 .. mt - 1, for mt below the sequence's query
+// tile count (whole query tiles only; rows is 32 or a multiple of 64).
+__device__ __forceinline__ int64_t tiles_before(int len, int mt, int rows, int causal) {
+  if (!causal) return static_cast<int64_t>(mt) * ((len + kBN - 1) / kBN);
+  if (rows >= kBN) return static_cast<int64_t>(rows / kBN) * mt * (mt + 1) / 2;
+  return (static_cast<int64_t>(mt) + 1) * (mt + 1) / 4;  // rows 32: sum of ceil(m / 2), m = 1..mt
+}
+__device__ __forceinline__ int64_t item_pos_in_seq(int len, int mt, int rows, int causal) {
+  return kUnits * tiles_before(len, mt, rows, causal) + static_cast<int64_t>(kItemUnits) * mt;
+}
+__device__ __forceinline__ int64_t seq_weight(int len, int rows, int causal) {
+  if (len <= 0) return 0;
+  const int n = (len + rows - 1) / rows;
+  return item_pos_in_seq(len, n - 1, rows, causal) +
+         kUnits * static_cast<int64_t>(item_tiles(len, n - 1, rows, causal)) + kItemUnits;
+}
+
+// One segment of a range: key tiles [j0, j1) of item (hg, rank r, mt),
+// wave-uniform.
+struct RangeSeg {
+  int valid;
+  int hg, r, mt;
+  int64_t P;       // the item's weight position
+  int64_t start;   // first row of its sequence
+  int len;         // the sequence's length
+  int n;           // its query tiles
+  int kt;          // key tiles of the item
+  int j0, j1;      // the tiles this range owns
+  int cut;         // its tiles span several ranges
 };
 
-template <int W>
-__device__ __forceinline__ SplitPlan plan_splits(const PrefillArgs& a, const int* s_len,
-                                                 const int* s_first, int T, int nwg, int* s_cls,
-                                                 int* s_wsum, unsigned long long* s_work) {
-  const int nm = a.n_mtiles;
-  const int tid = threadIdx.x;
-  SplitPlan p{nm, T, T};
-  if (!a.split_buf || !a.causal || 2 * nm > kScanMax) return p;
-  // Key tiles of all items, per head group.
-  if (tid == 0) *s_work = 0ull;
-  __syncthreads();
-  unsigned long long mine = 0;
-  for (int t = tid; t < a.num_seqs; t += W * 64) {
-    const int len = s_len[t];
-    for (int m0 = 0; m0 < len; m0 += a.rows) mine += (min(len, m0 + a.rows) + kBN - 1) / kBN;
+struct RangeCtx {
+  int64_t H;       // weight of one head group
+  int64_t U;       // total weight
+  int N;           // ranges
+  int v;           // this workgroup's range
+  int64_t p_lo, p_hi;  // its positions
+  int n_ranked;    // sequences of non-zero length (ranks 0 .. n_ranked - 1)
+  const int* rlen;
+  const int* rstart;
+  const int64_t* rpos;
+  // floor(p N / U), the range owning position p.  In double precision the
+  // quotient is exact here: p N < 2^53, and U < 2^43 keeps a non-integer
+  // quotient at least 2^-43 from the next integer, more than the rounding
+  // error (N 2^-53 <= 2^-43 for N <= 1024).
+  __device__ __forceinline__ int owner(int64_t p) const {
+    return static_cast<int>(__builtin_floor(static_cast<double>(p * N) / static_cast<double>(U)));
   }
-  if (mine) atomicAdd(s_work, mine);
-  __syncthreads();
-  const unsigned long long work = *s_work * a.groups;
-  const unsigned long long mean = (work + nwg - 1) / nwg;  // key tiles per workgroup
-  // Lowest mt with (mt + 1) rows > mean * 64 and at least four key tiles.
-  int ms = static_cast<int>(min<unsigned long long>(mean * kBN / a.rows, nm));
-  ms = max(ms, 4 * kBN / a.rows - 1);
-  auto before = [&](int r) { return r < nm ? s_first[r] : T; };  // items before rank r
-  while (ms < nm && before(nm - ms) > kMaxSplits) ++ms;
-  if (ms >= nm) return p;
-  p.ms = ms;
-  const int K = 2 * nm;
-  for (int j = tid; j < K; j += W * 64) {
-    const int k = K - j;
-    int cnt = 0;
-    const int mu = k / 2 - 1;  // whole items of query tile mu
-    if ((k & 1) == 0 && mu < ms) cnt += before(nm - mu) - before(nm - 1 - mu);
-    const int mp = k - 1;      // parts of the items of query tile mp
-    if (mp >= ms && mp < nm) cnt += 2 * (before(nm - mp) - before(nm - 1 - mp));
-    s_cls[j] = cnt;
-  }
-  __syncthreads();
-  p.E = block_exclusive_scan<W>(s_cls, K, s_wsum);
-  return p;
+};
+
+__device__ __forceinline__ int uread(const int* p) {
+  return __builtin_amdgcn_readfirstlane(*p);
+}
+__device__ __forceinline__ int64_t uread64(const int64_t* p) {
+  const uint64_t x = static_cast<uint64_t>(*p);
+  const uint32_t lo = __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(x));
+  const uint32_t hi = __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(x >> 32));
+  return static_cast<int64_t>((static_cast<uint64_t>(hi) << 32) | lo);
 }
 
-// Coordinates of work entry e (uniform): the item (seq, hg, mt), its part
-// (-1: whole) and split slot.
-__device__ __forceinline__ void entry_at(const PrefillArgs& a, const SplitPlan& p, int64_t e64,
-                                         const int* s_first, const int* s_sorted, const int* s_cls,
-                                         int& seq, int& hg, int& mt, int& part, int& slot) {
-  const int nm = a.n_mtiles;
-  part = -1;
-  slot = 0;
-  if (p.ms >= nm) {
-    item_at(a, e64, s_first, s_sorted, seq, hg, mt);
+// Fills kt and the tiles the range owns (item coordinates, P and the
+// sequence already set).
+__device__ __forceinline__ void own_tiles(const PrefillArgs& a, const RangeCtx& rc, RangeSeg& sg) {
+  sg.kt = item_tiles(sg.len, sg.mt, a.rows, a.causal);
+  sg.cut = 0;
+  if (sg.kt <= kAtomicTiles) {
+    const int64_t mid = sg.P + (kUnits * sg.kt + kItemUnits) / 2;
+    const bool own = mid >= rc.p_lo && mid < rc.p_hi;
+    sg.j0 = 0;
+    sg.j1 = own ? sg.kt : 0;
     return;
   }
-  const int e = __builtin_amdgcn_readfirstlane(static_cast<int>(e64));
-  const int K = 2 * nm;
-  int lo = 0, hi = K - 1;  // largest class index j with s_cls[j] <= e
+  const int64_t base = sg.P + kItemUnits + kUnits / 2;  // tile 0's midpoint
+  auto first_at = [&](int64_t p) -> int {  // first tile with midpoint >= p
+    if (p <= base) return 0;
+    const int64_t j = (p - base + kUnits - 1) / kUnits;
+    return static_cast<int>(j < sg.kt ? j : sg.kt);
+  };
+  sg.j0 = first_at(rc.p_lo);
+  sg.j1 = first_at(rc.p_hi);
+  sg.cut = sg.j0 < sg.j1 && (sg.j0 > 0 || sg.j1 < sg.kt);
+}
+
+// A cut item's first range (the one holding tile 0) and its number of
+// ranges.
+__device__ __forceinline__ void cut_ranges(const RangeCtx& rc, const RangeSeg& sg, int& vfirst,
+                                           int& nseg) {
+  const int64_t base = sg.P + kItemUnits + kUnits / 2;
+  vfirst = sg.j0 == 0 ? rc.v : rc.owner(base);
+  const int vlast =
+      sg.j1 == sg.kt ? rc.v : rc.owner(base + static_cast<int64_t>(kUnits) * (sg.kt - 1));
+  nseg = vlast - vfirst + 1;
+}
+
+__device__ __forceinline__ void seq_of_rank(const PrefillArgs& a, const RangeCtx& rc, RangeSeg& sg) {
+  sg.len = uread(rc.rlen + sg.r);
+  sg.start = uread(rc.rstart + sg.r);
+  sg.n = (sg.len + a.rows - 1) / a.rows;
+}
+
+// The item holding weight position p (0 <= p < U).
+__device__ __forceinline__ RangeSeg locate(const PrefillArgs& a, const RangeCtx& rc, int64_t p) {
+  RangeSeg sg;
+  sg.valid = 1;
+  sg.hg = static_cast<int>(p / rc.H);
+  const int64_t p1 = p - sg.hg * rc.H;
+  int lo = 0, hi = rc.n_ranked - 1;  // largest rank with pos <= p1
   while (lo < hi) {
     const int mid = (lo + hi + 1) >> 1;
-    if (__builtin_amdgcn_readfirstlane(s_cls[mid]) <= e) lo = mid; else hi = mid - 1;
+    if (uread64(rc.rpos + mid) <= p1) lo = mid; else hi = mid - 1;
   }
-  const int k = K - lo;
-  int o = e - __builtin_amdgcn_readfirstlane(s_cls[lo]);
-  auto before = [&](int r) {  // items before rank r
-    return r < nm ? __builtin_amdgcn_readfirstlane(s_first[r]) : p.T;
-  };
-  int r;
-  const int mu = k / 2 - 1;
-  bool whole = false;
-  if ((k & 1) == 0 && mu < p.ms) {
-    r = nm - 1 - mu;
-    const int n_whole = before(r + 1) - before(r);
-    whole = o < n_whole;
-    if (!whole) o -= n_whole;
+  sg.r = lo;
+  seq_of_rank(a, rc, sg);
+  const int64_t p2 = p1 - uread64(rc.rpos + lo);
+  int mlo = 0, mhi = sg.n - 1;  // largest query tile with f(mt) <= p2
+  while (mlo < mhi) {
+    const int mid = (mlo + mhi + 1) >> 1;
+    if (item_pos_in_seq(sg.len, mid, a.rows, a.causal) <= p2) mlo = mid; else mhi = mid - 1;
   }
-  int j;
-  if (whole) {
-    mt = mu;
-    j = o;
-  } else {
-    mt = k - 1;
-    r = nm - 1 - mt;
-    j = o >> 1;
-    part = o & 1;
-    slot = before(r) + j;
-  }
-  seq = __builtin_amdgcn_readfirstlane(s_sorted[j / a.groups]);
-  hg = j % a.groups;
+  sg.mt = mlo;
+  sg.P = p - p2 + item_pos_in_seq(sg.len, mlo, a.rows, a.causal);
+  own_tiles(a, rc, sg);
+  return sg;
 }
 
-// Small causal batches (fewer items than resident workgroups, so most CUs
-// would otherwise idle while the longest items finish): the same item list,
-// with the heaviest items cut in two (split plan above) and handed out in
-// the snake order of the persistent grid.  A part waits only for a part
-// that has finished its key tiles, so every wait ends.
+// The item after sg's (LDS is read only when it starts another sequence).
+__device__ __forceinline__ RangeSeg next_item(const PrefillArgs& a, const RangeCtx& rc,
+                                              const RangeSeg& sg) {
+  RangeSeg nx = sg;
+  nx.P = sg.P + static_cast<int64_t>(kUnits) * sg.kt + kItemUnits;
+  nx.valid = nx.P < rc.p_hi;
+  if (!nx.valid) return nx;
+  if (++nx.mt == sg.n) {
+    nx.mt = 0;
+    if (++nx.r == rc.n_ranked) {
+      nx.r = 0;
+      if (++nx.hg == a.groups) {
+        nx.valid = 0;
+        return nx;
+      }
+    }
+    seq_of_rank(a, rc, nx);
+  }
+  own_tiles(a, rc, nx);
+  return nx;
+}
+
+// sg itself if the range owns some of its tiles, else the next such item
+// (items the range does not own lie only at its two ends).
+__device__ __forceinline__ RangeSeg next_owned(const PrefillArgs& a, const RangeCtx& rc,
+                                               RangeSeg sg) {
+  while (sg.valid && sg.j0 >= sg.j1) sg = next_item(a, rc, sg);
+  return sg;
+}
+
+// Partial state hand-off of cut items.  Written and read with device-scope
+// accesses (sc1: through to, and from, the point where all XCDs' L2s
+// agree), so no L2 write-back or invalidation is needed (those stall the
+// whole XCD).  A part's saves complete (vmcnt(0)) before its ticket is
+// taken, and the part that takes the last ticket reads the others' saves
+// only after that, so it sees them whole.
+constexpr int kCpolDevice = 16;  // sc1
+
+template <int W>
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t slot_rsrc(const PrefillArgs& a, int slot) {
+  return __builtin_amdgcn_make_buffer_rsrc(a.slots + static_cast<int64_t>(slot) * slot_floats<W>(),
+                                           0, slot_floats<W>() * 4, 0x00020000);
+}
+
+template <int W>
+__device__ __forceinline__ void save_partial(__amdgpu_buffer_rsrc_t slot, int wave, int lane,
+                                             float m_run, float l_run, const q3::f32x16 (&acc)[4]) {
+#pragma unroll
+  for (int db = 0; db < 4; ++db)
+#pragma unroll
+    for (int r4 = 0; r4 < 4; ++r4) {
+      const q3::f32x4 v = {acc[db][4 * r4], acc[db][4 * r4 + 1], acc[db][4 * r4 + 2],
+                           acc[db][4 * r4 + 3]};
+      __builtin_amdgcn_raw_buffer_store_b128(
+          __builtin_bit_cast(q3::u32x4, v), slot,
+          static_cast<uint32_t>(((wave * 16 + db * 4 + r4) * 64 + lane) * 16), 0, kCpolDevice);
+    }
+  const uint32_t ml = slot_ml_offset<W>() + (wave * 64 + lane) * 8;
+  __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(m_run), slot, ml, 0, kCpolDevice);
+  __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(l_run), slot, ml + 4, 0, kCpolDevice);
+}
+
+// Folds a saved part into (m_run, l_run, acc): the state becomes relative
+// to the larger running max, state * 2^(m_state - m) + part * 2^(m_part - m).
+// Parts are folded in key order, so the bits depend only on the parts.  The
+// accumulators go in two halves of 32 (one memory round trip each).
+template <int W>
+__device__ __forceinline__ void fold_partial(__amdgpu_buffer_rsrc_t slot, int wave, int lane,
+                                             float& m_run, float& l_run, q3::f32x16 (&acc)[4]) {
+  const uint32_t ml = slot_ml_offset<W>() + (wave * 64 + lane) * 8;
+  const float om = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(slot, ml, 0, kCpolDevice));
+  const float ol =
+      __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(slot, ml + 4, 0, kCpolDevice));
+  const float m = fmaxf(m_run, om);
+  const float m_use = m == q3::kNegInf ? 0.f : m;
+  const float a_s = q3::fast_exp2(m_run - m_use);  // exp2(-inf) = 0: an empty side adds nothing
+  const float a_p = q3::fast_exp2(om - m_use);
+  m_run = m;
+  l_run = __builtin_fmaf(ol, a_p, l_run * a_s);
+#pragma unroll
+  for (int half = 0; half < 2; ++half) {
+    q3::f32x4 x[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i)
+      x[i] = __builtin_bit_cast(
+          q3::f32x4, __builtin_amdgcn_raw_buffer_load_b128(
+                         slot, static_cast<uint32_t>(((wave * 16 + 8 * half + i) * 64 + lane) * 16),
+                         0, kCpolDevice));
+#pragma unroll
+    for (int i = 0; i < 8; ++i)
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const int k = 8 * half + i;
+        const float y = acc[k >> 2][4 * (k & 3) + e];
+        acc[k >> 2][4 * (k & 3) + e] = __builtin_fmaf(x[i][e], a_p, y * a_s);
+      }
+  }
+}
+
+template <int W>
+__device__ __forceinline__ void load_partial(__amdgpu_buffer_rsrc_t slot, int wave, int lane,
+                                             float& m_run, float& l_run, q3::f32x16 (&acc)[4]) {
+  const uint32_t ml = slot_ml_offset<W>() + (wave * 64 + lane) * 8;
+  m_run = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(slot, ml, 0, kCpolDevice));
+  l_run = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(slot, ml + 4, 0, kCpolDevice));
+#pragma unroll
+  for (int i = 0; i < 16; ++i) {
+    const q3::f32x4 x = __builtin_bit_cast(
+        q3::f32x4, __builtin_amdgcn_raw_buffer_load_b128(
+                       slot, static_cast<uint32_t>(((wave * 16 + i) * 64 + lane) * 16), 0,
+                       kCpolDevice));
+#pragma unroll
+    for (int e = 0; e < 4; ++e) acc[i >> 2][4 * (i & 3) + e] = x[e];
+  }
+}
+
+// Range grid (CUs x resident workgroups, a multiple of 8): range v of N
+// (ranges of workgroups on one XCD adjacent when every workgroup has one)
+// is streamed as a chain of segments.  The first K/V tile and the Q rows
+// of the next segment load during the current segment's last tile, so a
+// segment start costs no memory round trip.  A segment of a cut item
+// saves its partial state in slot 2 v (the range's first segment) or
+// 2 v + 1 (its last, the part holding the item's tile 0), then takes the
+// item's ticket; the part taking the last ticket folds every part in key
+// order and writes the output.  The part holding tile 0 (normally the
+// last to finish: it ends its range) first checks the ticket and, when the
+// others are all in, folds without saving.  No part waits for another.
 template <int W>
 __global__ __launch_bounds__(W * 64) __attribute__((amdgpu_waves_per_eu(2, 2)))
-void varlen_prefill_split_kernel(PrefillArgs a) {
+void varlen_prefill_range_kernel(PrefillArgs a) {
   Q3_PREFILL_TILE_BUFFERS;
-  __shared__ int s_len[kMaxSeqs];
-  __shared__ int s_start[kMaxSeqs];
-  __shared__ int s_sorted[kMaxSeqs];
-  __shared__ int s_first[kScanMax];  // items before m-tile rank r (r = n_mtiles-1-mt)
-  __shared__ int s_cls[kScanMax];    // entries before work class 2 n_mtiles - j
-  __shared__ int s_wsum[W];
-  __shared__ unsigned long long s_work;
-  __shared__ uint32_t s_role;
-  const int T_items = build_items<W>(a, s_len, s_start, s_sorted, s_first, s_wsum);
-  const SplitPlan plan =
-      plan_splits<W>(a, s_len, s_first, T_items, gridDim.x, s_cls, s_wsum, &s_work);
-  const int64_t nwg = gridDim.x;
+  __shared__ int s_rlen[kMaxSeqs];
+  __shared__ int s_rstart[kMaxSeqs];
+  __shared__ int64_t s_rpos[kMaxSeqs + 1];
+  __shared__ uint32_t s_ticket;
+  static_assert(kMaxSeqs == 4 * 64, "one wave scans the ranked weights, four per lane");
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int S = a.num_seqs;
+  // ---- sequence tables: lengths ranked longest first, weight prefix ----
+  int* s_len0 = reinterpret_cast<int*>(s_k0);  // tile buffers are free until the first load
+  int* s_start0 = reinterpret_cast<int*>(s_v0);
+  for (int t = tid; t < S; t += W * 64) {
+    const int64_t s0 = a.cu[t], s1 = a.cu[t + 1];
+    const bool ok = s0 >= 0 && s1 <= a.total && s1 > s0;
+    s_len0[t] = ok ? static_cast<int>(s1 - s0) : 0;
+    s_start0[t] = ok ? static_cast<int>(s0) : 0;
+  }
+  __syncthreads();
+  for (int t = tid; t < S; t += W * 64) {
+    const int lt = s_len0[t];
+    int rank = 0;
+    for (int u = 0; u < S; ++u) {
+      const int lu = s_len0[u];
+      rank += (lu > lt || (lu == lt && u < t)) ? 1 : 0;
+    }
+    s_rlen[rank] = lt;
+    s_rstart[rank] = s_start0[t];
+  }
+  __syncthreads();
+  if (wave == 0) {
+    int64_t w4[4], sum = 0;
+    int nz = 0;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int r = lane * 4 + i;
+      const int len = r < S ? s_rlen[r] : 0;
+      w4[i] = seq_weight(len, a.rows, a.causal);
+      sum += w4[i];
+      nz += len > 0 ? 1 : 0;
+    }
+    int64_t incl = sum;
+#pragma unroll
+    for (int o = 1; o < 64; o <<= 1) {
+      const int64_t y = __shfl_up(incl, o, 64);
+      if (lane >= o) incl += y;
+    }
+    int64_t run = incl - sum;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int r = lane * 4 + i;
+      if (r < kMaxSeqs) s_rpos[r] = run;
+      run += w4[i];
+    }
+#pragma unroll
+    for (int o = 32; o >= 1; o >>= 1) nz += __shfl_xor(nz, o, 64);
+    if (lane == 63) s_rpos[kMaxSeqs] = incl;
+    if (lane == 0) s_ticket = static_cast<uint32_t>(nz);
+  }
+  __syncthreads();
+  RangeCtx rc;
+  rc.rlen = s_rlen;
+  rc.rstart = s_rstart;
+  rc.rpos = s_rpos;
+  rc.H = uread64(s_rpos + kMaxSeqs);
+  rc.n_ranked = static_cast<int>(__builtin_amdgcn_readfirstlane(s_ticket));
+  rc.U = rc.H * a.groups;
+  if (rc.U == 0) return;
+  const int nwg = gridDim.x;
+  int64_t N = rc.U / (kMinRangeTiles * kUnits);
+  N = N < 1 ? 1 : N;
+  N = N < nwg ? N : nwg;
+  N = N < a.max_ranges ? N : a.max_ranges;
+  rc.N = static_cast<int>(N);
   const int w = blockIdx.x;
-  const int w_mirror = (gridDim.x / 8 - 1 - w / 8) * 8 + w % 8;
-  int64_t i = w;
-  for (int round = 1; i < plan.E; ++round) {
-    int seq, hg, mt, part, slot;
-    entry_at(a, plan, i, s_first, s_sorted, s_cls, seq, hg, mt, part, slot);
-    const int64_t start = a.cu[seq];  // a valid range: the entry exists
-    prefill_item<W, true>(a, off, start, static_cast<int>(a.cu[seq + 1] - start), hg, mt, tb,
-                          part, slot, &s_role);
-    i = static_cast<int64_t>(round) * nwg + ((round & 1) ? w_mirror : w);
-    __syncthreads();  // the entry's LDS tiles are no longer read
+  // every workgroup busy: XCD x (workgroups w % 8 == x) holds ranges
+  // x * nwg / 8 .. , adjacent items sharing its L2; fewer ranges: spread.
+  const int v = rc.N == nwg && nwg % 8 == 0 ? (w % 8) * (nwg / 8) + w / 8 : w;
+  if (v >= rc.N) return;
+  rc.v = v;
+  rc.p_lo = (static_cast<int64_t>(v) * rc.U + rc.N - 1) / rc.N;
+  rc.p_hi = (static_cast<int64_t>(v + 1) * rc.U + rc.N - 1) / rc.N;
+  __syncthreads();  // s_ticket is reused below
+  if (rc.p_lo >= rc.p_hi) return;
+
+  const uint32_t o_lane = o_lane_offset(a, lane);
+  for (RangeSeg cur = next_owned(a, rc, locate(a, rc, rc.p_lo)); cur.valid;
+       cur = next_owned(a, rc, next_item(a, rc, cur))) {
+    const WaveItem wi = wave_item<W>(a, cur.start, cur.len, cur.hg, cur.mt, wave, lane);
+    float m_run, l_run;
+    q3::f32x16 acc[4];  // acc[db][r] = O[q0 + l32][32*db + 8*(r/4) + 4*hl + r%4]
+    run_tiles<W>(a, off, wi, cur.j0, cur.j1, tb, lane, wave, m_run, l_run, acc);
+    bool write = !cur.cut;
+    if (cur.cut) {
+      int vfirst, nseg;
+      cut_ranges(rc, cur, vfirst, nseg);
+      uint32_t* ticket = a.tickets + vfirst;
+      const bool first_part = v == vfirst;  // holds tile 0, ends this range
+      const uint32_t last = static_cast<uint32_t>(nseg - 1);
+      bool merged = false;
+      if (first_part) {
+        if (tid == 0) s_ticket = __hip_atomic_load(ticket, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        __syncthreads();
+        if (s_ticket == last) {  // every other part has saved: fold them in without saving
+          for (int p = 1; p < nseg; ++p)
+            fold_partial<W>(slot_rsrc<W>(a, 2 * (vfirst + p)), wave, lane, m_run, l_run, acc);
+          merged = true;
+        }
+        __syncthreads();  // s_ticket is reused below
+      }
+      if (!merged) {
+        save_partial<W>(slot_rsrc<W>(a, first_part ? 2 * v + 1 : 2 * v), wave, lane, m_run, l_run,
+                        acc);
+        wait_loads();  // this wave's saves are complete
+        __syncthreads();
+        if (tid == 0)
+          s_ticket = __hip_atomic_fetch_add(ticket, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        __syncthreads();
+        if (s_ticket == last) {  // the last part in: fold all saved parts, in key order
+          load_partial<W>(slot_rsrc<W>(a, 2 * vfirst + 1), wave, lane, m_run, l_run, acc);
+          for (int p = 1; p < nseg; ++p)
+            fold_partial<W>(slot_rsrc<W>(a, 2 * (vfirst + p)), wave, lane, m_run, l_run, acc);
+          merged = true;
+        }
+      }
+      if (merged && tid == 0)
+        __hip_atomic_store(ticket, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      write = merged;
+    }
+    if (write) {
+      l_run = cross_half_sum(l_run);
+      if (wi.active()) store_output(a, wi, lane, o_lane, l_run, acc, stage_of(tb, wave));
+    }
+    __syncthreads();  // the staging buffers are read before the next segment's loads refill them
   }
 }
 
+// Resident workgroups per CU of a kernel, queried once per device (a
+// host-side cost of every call otherwise).
+template <int W>
+int resident_per_cu(const void* kernel, int dev, int* cache) {
+  int per_cu = dev >= 0 && dev < 64 ? cache[dev] : 0;
+  if (per_cu == 0 &&
+      hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kernel, W * 64, 0) == hipSuccess &&
+      per_cu > 0 && dev >= 0 && dev < 64)
+    cache[dev] = per_cu;
+  return per_cu;
+}
+
+// Sizes the items for W waves and launches the range grid (four waves,
+// given a workspace, fewer items than resident workgroups), the persistent
+// grid (CUs x resident workgroups, from the occupancy API) or, past their
+// LDS tables, the flat grid.
 template <int W>
 int launch_prefill(PrefillArgs a, int num_seqs, int max_seqlen, int dev, int cus,
                    hipStream_t s, const char* who) {
@@ -949,27 +1207,35 @@ int launch_prefill(PrefillArgs a, int num_seqs, int max_seqlen, int dev, int cus
   if (blocks > 0x7fffffff)
     return q3::fail(QWEN3_EINVAL, "%s: grid too large (heads %d, seqs %d, max_seqlen %d)", who,
                     a.Hq, num_seqs, max_seqlen);
-  // Resident workgroups per CU, queried once per device (a host-side cost
-  // of every call otherwise).
-  static int occupancy[64] = {0};
-  int per_cu = dev >= 0 && dev < 64 ? occupancy[dev] : 0;
-  if (per_cu == 0 &&
-      hipOccupancyMaxActiveBlocksPerMultiprocessor(
-          &per_cu, reinterpret_cast<const void*>(varlen_prefill_persistent_kernel<W>), W * 64,
-          0) == hipSuccess &&
-      per_cu > 0 && dev >= 0 && dev < 64)
-    occupancy[dev] = per_cu;
-  const bool persistent =
-      num_seqs <= kMaxSeqs && a.n_mtiles <= kScanMax && cus > 0 && per_cu > 0;
+  static int occ_persistent[64] = {0};
+  static int occ_range[64] = {0};
   // At most this many items: groups x (query tiles of all rows + one
   // ragged tile per sequence).
   const int64_t items_max = static_cast<int64_t>(a.groups) *
                             (q3::cdiv(a.total, a.rows) + static_cast<int64_t>(num_seqs));
-  if (persistent && a.split_buf && a.causal && 2 * a.n_mtiles <= kScanMax &&
-      items_max < static_cast<int64_t>(cus) * per_cu) {
-    const int wgs = ((cus * per_cu + 7) / 8) * 8;
-    hipLaunchKernelGGL(varlen_prefill_split_kernel<W>, dim3(wgs), dim3(W * 64), 0, s, a);
-  } else if (persistent) {
+  if constexpr (W == 4) {
+    // Fewer items than resident workgroups (a few long prompts): the range
+    // schedule, which cuts the heaviest items across workgroups.  With
+    // more, whole items in the persistent grid finish sooner: an item
+    // switch costs about 2.5 tiles' time and a cut item more, which the
+    // better balance of equal ranges does not win back (measured on the
+    // Qwen3-0.6B batch: 59 us persistent against 70 us in ranges).
+    if (a.tickets && num_seqs <= kMaxSeqs && cus > 0) {
+      const int per_cu = resident_per_cu<W>(
+          reinterpret_cast<const void*>(varlen_prefill_range_kernel<W>), dev, occ_range);
+      const int wgs = (cus * per_cu) / 8 * 8;
+      a.max_ranges = a.max_ranges < wgs ? a.max_ranges : wgs;
+      if (per_cu > 0 && a.max_ranges > 0 && items_max < static_cast<int64_t>(cus) * per_cu) {
+        hipLaunchKernelGGL(varlen_prefill_range_kernel<W>, dim3(wgs), dim3(W * 64), 0, s, a);
+        return q3::launch_status(who);
+      }
+    }
+  }
+  const int per_cu = resident_per_cu<W>(
+      reinterpret_cast<const void*>(varlen_prefill_persistent_kernel<W>), dev, occ_persistent);
+  const bool persistent =
+      num_seqs <= kMaxSeqs && a.n_mtiles <= kScanMax && cus > 0 && per_cu > 0;
+  if (persistent) {
     const int wgs = ((cus * per_cu + 7) / 8) * 8;  // multiple of 8 for the XCD-preserving snake
     hipLaunchKernelGGL(varlen_prefill_persistent_kernel<W>, dim3(wgs), dim3(W * 64), 0, s, a);
   } else {
@@ -979,16 +1245,34 @@ int launch_prefill(PrefillArgs a, int num_seqs, int max_seqlen, int dev, int cus
   return q3::launch_status(who);
 }
 
-// Workspace: schedule counters, split tickets / flags, then split partials.
+// Workspace: schedule counters, then range tickets, then range slots; the
+// range part is sized for two four-wave workgroups per CU.
 constexpr size_t kCtrBytes = (kPools + 1) * kPoolStride * sizeof(uint32_t);
-constexpr size_t kSplitCtrBytes = kMaxSplits * 2 * sizeof(uint32_t);
-constexpr size_t kSplitBufOffset = (kCtrBytes + kSplitCtrBytes + 255) / 256 * 256;
-constexpr size_t kWorkspaceBytes =
-    kSplitBufOffset + static_cast<size_t>(kMaxSplits) * kSplitSlotFloats * sizeof(float);
+constexpr int kMaxCus = 1024;
+size_t ranges_for(int cus) { return static_cast<size_t>(2) * static_cast<size_t>(cus); }
+size_t ticket_bytes(size_t ranges) { return (ranges * sizeof(uint32_t) + 255) / 256 * 256; }
+size_t workspace_bytes_for(int cus) {
+  const size_t n = ranges_for(cus);
+  return kCtrBytes + ticket_bytes(n) + 2 * n * slot_floats<4>() * sizeof(float);
+}
+
+int device_cus() {
+  static int cu_cache[64] = {0};
+  int dev = -1, cus = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0) return 0;
+  if (dev < 64 && cu_cache[dev]) return cu_cache[dev];
+  if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess)
+    return 0;
+  if (dev < 64) cu_cache[dev] = cus;
+  return cus;
+}
 
 }  // namespace
 
-extern "C" size_t qwen3_varlen_prefill_workspace_bytes(void) { return kWorkspaceBytes; }
+extern "C" size_t qwen3_varlen_prefill_workspace_bytes(void) {
+  const int cus = device_cus();
+  return workspace_bytes_for(cus > 0 && cus <= kMaxCus ? cus : 256);
+}
 
 extern "C" int qwen3_varlen_prefill_bf16(const void* q, const int64_t q_strides[2],
                                          const void* k, const int64_t k_strides[2],
@@ -1042,40 +1326,36 @@ extern "C" int qwen3_varlen_prefill_bf16(const void* q, const int64_t q_strides[
   a.scale_log2 = scale * q3::kLog2e;
   a.causal = causal ? 1 : 0;
   a.groups = num_heads / a.HG;
+  const int cus = device_cus();
   if (workspace) {
-    if (workspace_bytes < qwen3_varlen_prefill_workspace_bytes())
+    const size_t need = workspace_bytes_for(cus > 0 && cus <= kMaxCus ? cus : 256);
+    if (workspace_bytes < need)
       return q3::fail(QWEN3_EWORKSPACE, "%s: workspace of %zu bytes needed, %zu given", who,
-                      qwen3_varlen_prefill_workspace_bytes(), workspace_bytes);
+                      need, workspace_bytes);
     if (!q3::aligned16(workspace))
       return q3::fail(QWEN3_EALIGN, "%s: workspace must be 16-byte aligned", who);
   }
 
   q3::clear_error();
   hipStream_t s = static_cast<hipStream_t>(stream);
-  int dev = -1, cus = 0;
-  static int cu_cache[64] = {0};
-  if (hipGetDevice(&dev) == hipSuccess && dev >= 0 && dev < 64) {
-    cus = cu_cache[dev];
-    if (cus == 0 &&
-        hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess)
-      cu_cache[dev] = cus;
-  }
+  int dev = -1;
+  if (hipGetDevice(&dev) != hipSuccess) dev = -1;
   // Eight-wave workgroups once the batch holds enough of their (twice as
   // large) work items to give every CU four: they halve the K/V tile
-  // traffic per flop, but a batch of a few short sequences needs the finer
-  // four-wave items to spread its causal work.
+  // traffic per flop; smaller batches take the range schedule of four-wave
+  // workgroups, which cuts the heaviest items across workgroups.
   const int64_t rows8 = 32 * 8 / a.HG;
   const int64_t items8 = static_cast<int64_t>(a.groups) * q3::cdiv(total_tokens, rows8);
   const bool wide = cus > 0 && items8 >= 4 * static_cast<int64_t>(cus);
-  // Items handed out from the counters only on the eight-wave path: over
-  // many rounds of mixed-length items they finish 1-2% sooner (64 prompts
-  // of 128..1024 tokens: 229 -> 224 us), while the few rounds of a small
-  // batch are paired better by the static snake.
-  if (workspace && wide) a.ctr = static_cast<uint32_t*>(workspace);
   if (workspace) {
     char* ws = static_cast<char*>(workspace);
-    a.split_ctr = reinterpret_cast<uint32_t*>(ws + kCtrBytes);
-    a.split_buf = reinterpret_cast<float*>(ws + kSplitBufOffset);
+    // Items handed out from the counters only on the eight-wave path: over
+    // many rounds of mixed-length items they finish 1-2% sooner.
+    if (wide) a.ctr = reinterpret_cast<uint32_t*>(ws);
+    const size_t n = ranges_for(cus > 0 && cus <= kMaxCus ? cus : 256);
+    a.tickets = reinterpret_cast<uint32_t*>(ws + kCtrBytes);
+    a.slots = reinterpret_cast<float*>(ws + kCtrBytes + ticket_bytes(n));
+    a.max_ranges = static_cast<int>(n);
   }
   return wide ? launch_prefill<8>(a, num_seqs, max_seqlen, dev, cus, s, who)
               : launch_prefill<4>(a, num_seqs, max_seqlen, dev, cus, s, who);

@@ -16,14 +16,18 @@ __all__ = ["flash_attention_prefill", "flash_attention_prefill_batched"]
 _WORKSPACES: dict = {}
 
 
-def _schedule_workspace(device, lib) -> torch.Tensor:
-    """The per-device workspace of the dynamic item schedule and the split
-    items, zeroed once (each call leaves its counters at zero)."""
-    ws = _WORKSPACES.get(device)
+def _schedule_workspace(device, stream: int, lib) -> torch.Tensor:
+    """The workspace of the item counters and of the items cut across
+    workgroups (tickets and partial states) for this device and stream,
+    zeroed once (every call leaves its counters and tickets at zero).  One
+    per stream: calls on different streams may run at the same time and
+    must not share tickets."""
+    key = (str(device), stream)
+    ws = _WORKSPACES.get(key)
     if ws is None:
         ws = torch.zeros(int(lib.qwen3_varlen_prefill_workspace_bytes()), dtype=torch.uint8,
                          device=device)
-        _WORKSPACES[device] = ws
+        _WORKSPACES[key] = ws
     return ws
 
 
@@ -42,10 +46,11 @@ def flash_attention_prefill(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
     the reference's device->host read of cu_seqlens (:177-178); when omitted
     it is computed the same way the reference does.  A given max_seqlen must
     bound every sequence: rows of a longer one past max_seqlen (rounded up to
-    a query tile) are left unwritten.  `workspace`: the dynamic schedule's
-    counters and the split items' partial states (default: one zeroed buffer
-    per device, kept by this module; concurrent calls on several streams
-    pass their own, zeroed once).
+    a query tile) are left unwritten.  `workspace`: the item counters and
+    the tickets and partial states of items cut across workgroups
+    (qwen3_varlen_prefill_workspace_bytes() bytes, zeroed once; default: one
+    per device and stream, kept by this module).  Without a workspace no
+    item is cut: each runs whole in one workgroup.
     """
     assert q.dim() == 3 and q.shape[1] == num_heads and q.shape[2] == head_dim
     assert k.shape == (q.shape[0], num_kv_heads, head_dim) and v.shape == k.shape
@@ -69,8 +74,9 @@ def flash_attention_prefill(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
             "out must be a bf16 (total_tokens, num_heads, head_dim) tensor with unit last stride"
         _lib.require_hip(out)
     lib = _lib.load()
+    stream = _lib.stream_of(dev)
     if workspace is None:
-        workspace = _schedule_workspace(q.device, lib)
+        workspace = _schedule_workspace(q.device, stream, lib)
     rc = lib.qwen3_varlen_prefill_bf16(
         q.data_ptr(), _lib.strides(q, (0, 1)),
         k.data_ptr(), _lib.strides(k, (0, 1)),
@@ -78,7 +84,7 @@ def flash_attention_prefill(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
         out.data_ptr(), _lib.strides(out, (0, 1)),
         cu_seqlens.data_ptr(), num_seqs, int(max_seqlen), q.shape[0],
         num_heads, num_kv_heads, head_dim, float(scale), 1 if causal else 0,
-        workspace.data_ptr(), workspace.numel(), _lib.stream_of(dev))
+        workspace.data_ptr(), workspace.numel(), stream)
     _lib.check(rc, "qwen3_varlen_prefill_bf16")
     return out
 

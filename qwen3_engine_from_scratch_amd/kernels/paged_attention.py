@@ -29,12 +29,13 @@ __all__ = [
 ]
 
 
-def paged_decode_workspace_bytes(batch: int, num_heads: int, head_dim: int,
+def paged_decode_workspace_bytes(batch: int, num_heads: int, num_kv_heads: int, head_dim: int,
                                  max_pages: int, block_size: int) -> int:
-    """Split-KV workspace size; depends only on the launch shape, so a graph
-    captured once stays valid for any live context lengths."""
+    """Split-KV workspace size on the current device; depends only on the
+    launch shape, so a graph captured once stays valid for any live context
+    lengths."""
     return int(_lib.load().qwen3_paged_decode_workspace_bytes(
-        batch, num_heads, head_dim, max_pages, block_size))
+        batch, num_heads, num_kv_heads, head_dim, max_pages, block_size))
 
 
 def paged_attention_decode_hip(q, k_buffer, v_buffer, block_table_2d,
@@ -84,7 +85,8 @@ def paged_attention_decode_hip(q, k_buffer, v_buffer, block_table_2d,
             "out must be a bf16 (B, num_heads, head_dim) tensor with unit last stride"
         _lib.require_hip(out)
     max_rows, max_pages = block_table_2d.shape
-    need = paged_decode_workspace_bytes(B, num_heads, head_dim, max_pages, block_size)
+    need = paged_decode_workspace_bytes(B, num_heads, num_kv_heads, head_dim, max_pages,
+                                        block_size)
     if workspace is None or workspace.numel() < need:
         workspace = torch.empty(max(need, 1), dtype=torch.uint8, device=dev)
     lib = _lib.load()

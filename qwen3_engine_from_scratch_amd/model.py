@@ -168,6 +168,7 @@ class Qwen3ForCausalLM(nn.Module):
         """Allocates the split-KV workspace of the decode attention for up to
         `batch` rows once (a captured graph keeps using it)."""
         need = paged_decode_workspace_bytes(batch, self.config.num_attention_heads,
+                                            self.config.num_key_value_heads,
                                             self.config.head_dim, pool.block_table_2d.shape[1],
                                             pool.block_size)
         if self._workspace is None or self._workspace.numel() < need:

@@ -36,22 +36,34 @@ def test_library_exports_every_declared_symbol():
     assert lib.qwen3_attn_abi_version() == _lib.ABI_VERSION
 
 
+def _cus() -> int:
+    """CUs of the visible device (0 when there is none)."""
+    import torch
+    return torch.cuda.get_device_properties(0).multi_processor_count if torch.cuda.is_available() else 0
+
+
 def test_workspace_bytes():
     lib = _lib.load()
     def a256(x):
         return -(-x // 256) * 256
 
-    # batches up to 2048: two (128 + 1)-float partial slots per wave for up to
-    # 4096 waves x 16 query columns, plus the (B + 1)-entry tile prefix
-    waves = 4096
-    expect = a256(waves * 2 * 16 * 128 * 4) + a256(waves * 2 * 16 * 4) + a256(257 * 4) + 256
-    assert lib.qwen3_paged_decode_workspace_bytes(256, 32, 128, 512, 16) == expect
+    # batches up to 2048: two (128 + 1)-float partial slots per wave and
+    # query head of the group, plus the (B + 1)-entry tile prefix: two
+    # four-wave workgroups per CU of the current device, or the largest grid
+    # (1024 workgroups) when no device can be queried
+    waves = 4 * (min(2 * _cus(), 1024) if _cus() else 1024)
+    for hq, hkv in ((32, 8), (16, 8), (16, 1)):
+        G = hq // hkv
+        expect = a256(waves * 2 * G * 128 * 4) + a256(waves * 2 * G * 4) + a256(257 * 4) + 256
+        assert lib.qwen3_paged_decode_workspace_bytes(256, hq, hkv, 128, 512, 16) == expect
     # larger batches: one partial per (b, query head, 2048-token partition)
     slots = 4096 * 32 * -(-512 * 16 // 2048)
-    assert lib.qwen3_paged_decode_workspace_bytes(4096, 32, 128, 512, 16) == \
+    assert lib.qwen3_paged_decode_workspace_bytes(4096, 32, 8, 128, 512, 16) == \
         a256(slots * 128 * 4) + a256(slots * 4)
-    assert lib.qwen3_paged_decode_workspace_bytes(4, 16, 64, 64, 16) == 0  # head_dim 64 not built
-    assert lib.qwen3_paged_decode_workspace_bytes(4, 16, 128, 64, 8) == 0  # block_size 8
+    assert lib.qwen3_paged_decode_workspace_bytes(4, 16, 8, 64, 64, 16) == 0  # head_dim 64 not built
+    assert lib.qwen3_paged_decode_workspace_bytes(4, 16, 8, 128, 64, 8) == 0  # block_size 8
+    assert lib.qwen3_paged_decode_workspace_bytes(4, 16, 3, 128, 64, 16) == 0  # 16 % 3 != 0
+    assert lib.qwen3_paged_decode_workspace_bytes(4, 34, 2, 128, 64, 16) == 0  # G = 17
 
 
 def _s(*v):
@@ -96,9 +108,11 @@ def test_prefill_rejects_bad_arguments():
                                              FAKE, 2, 100, 150, H, Hk, D, 0.088, 1, ws, wsb, None)
 
     need = lib.qwen3_varlen_prefill_workspace_bytes()
-    # 9 schedule counters 128 B apart, 256 split slots' (ticket, flag), then
-    # 256-aligned, 256 slots of 8 waves x 64 lanes x 66 floats
-    assert need == 3328 + 256 * 8 * 64 * 66 * 4
+    # 9 schedule counters 128 B apart, then for two ranges per CU (256 CUs
+    # when no device is visible) one ticket each (256-aligned) and two
+    # partial-state slots each of 4 waves x 64 lanes x 66 floats
+    ranges = 2 * (_cus() or 256)
+    assert need == 1152 + -(-ranges * 4 // 256) * 256 + 2 * ranges * 4 * 64 * 66 * 4
     assert call(ws=FAKE, wsb=need - 1) == -4  # a schedule workspace too small
     assert call(D=256) == -3
     assert call(H=12, Hk=8) == -3

@@ -242,7 +242,7 @@ def test_decode_garbage_workspace_same_bits(gpu, B, lo, hi):
     lens = [int(x) for x in torch.randint(lo, hi, (B,), generator=g)]
     announce(f"decode garbage workspace B={B} lens in [{lo},{hi})")
     t = make_device_decode(lens, 16, 8, gpu, seed=B, slack=0.1)
-    need = paged_decode_workspace_bytes(B, 16, 128, t["bt"].shape[1], 16)
+    need = paged_decode_workspace_bytes(B, 16, 8, 128, t["bt"].shape[1], 16)
     outs = []
     ws = None
     for fill in (0, 255, None):

@@ -1,4 +1,6 @@
 """Varlen prefill kernel vs the oracle / fp32 references on the GPU."""
+from types import SimpleNamespace
+
 import pytest
 import torch
 
@@ -148,12 +150,13 @@ def test_prefill_many_sequences_flat_grid(gpu, n, lo, hi):
 
 
 def test_prefill_counter_schedule_matches_static(gpu):
-    """The item counters (a workspace) only reorder work: the output is the
-    same bits as the static order's, the counters end at zero, and a
+    """Eight-wave workgroups (a batch of at least four of their items per
+    CU): the item counters (a workspace) only reorder work, so the output is
+    the same bits as the static order's, the counters end at zero, and a
     workspace holding garbage gives the same result."""
     from qwen3_engine_from_scratch_amd import _lib
 
-    lens, hq, hkv = [4000, 4000, 4000, 4000], 16, 8
+    lens, hq, hkv = [4096] * 8, 16, 8
     c = oi.make_prefill_case(lens, hq, hkv, 128, seed=7)
     q, k, v = c.q.to(gpu), c.k.to(gpu), c.v.to(gpu)
     cu = c.cu_seqlens.to(gpu)
@@ -182,51 +185,105 @@ def test_prefill_counter_schedule_matches_static(gpu):
     assert torch.equal(call(ws), static)
 
 
-SPLIT_CTR = slice(1152, 3200)  # split tickets / ready flags inside the workspace
-SPLIT_BUF = 3328                # first byte of the split partials
+TICKETS = 1152  # first byte of the range tickets inside the workspace
 
 
-@pytest.mark.parametrize("lens,hq,hkv", [
-    ([2048], 16, 8),
-    ([1500, 700], 16, 8),
-    ([1200], 32, 8),   # G = 4: 32-row items
-    ([2500], 8, 8),    # G = 1: 128-row items
-])
-def test_prefill_split_items_vs_fp32(gpu, lens, hq, hkv):
-    """Causal batches with fewer work items than resident workgroups take the
-    split kernel: the heaviest items are cut into two key ranges whose
-    partial softmax states meet in the workspace.  The output matches the
-    fp32 closed form, repeated calls give the same bits whichever part
-    finishes first, and every call leaves the split tickets and flags at
-    zero."""
+def _layout(lib):
+    """(ticket bytes, first slot byte) of the workspace on this device."""
+    need = int(lib.qwen3_varlen_prefill_workspace_bytes())
+    slot = 4 * 64 * 66 * 4
+    ranges = (need - TICKETS) // (4 + 2 * slot)
+    tb = (ranges * 4 + 255) // 256 * 256
+    assert need == TICKETS + tb + 2 * ranges * slot
+    return slice(TICKETS, TICKETS + tb), TICKETS + tb
+
+
+def _call(lib, gpu, c, hq, hkv, ws, causal=True):
     from qwen3_engine_from_scratch_amd import _lib
 
-    c = oi.make_prefill_case(lens, hq, hkv, 128, seed=sum(lens) % 97)
     q, k, v = c.q.to(gpu), c.k.to(gpu), c.v.to(gpu)
     cu = c.cu_seqlens.to(gpu)
+    out = torch.empty_like(q)
+    rc = lib.qwen3_varlen_prefill_bf16(
+        q.data_ptr(), _lib.strides(q, (0, 1)), k.data_ptr(), _lib.strides(k, (0, 1)),
+        v.data_ptr(), _lib.strides(v, (0, 1)), out.data_ptr(), _lib.strides(out, (0, 1)),
+        cu.data_ptr(), len(c.lens), max(c.lens), q.shape[0], hq, hkv, 128, c.scale,
+        1 if causal else 0, None if ws is None else ws.data_ptr(), 0 if ws is None else ws.numel(),
+        _lib.stream_of(gpu))
+    _lib.check(rc, "qwen3_varlen_prefill_bf16")
+    torch.cuda.synchronize()
+    return out
+
+
+@pytest.mark.parametrize("lens,hq,hkv,causal", [
+    ([2048], 16, 8, True),               # one long prompt: items cut into up to five parts
+    ([1500, 700], 16, 8, True),
+    ([1200], 32, 8, True),               # G = 4: 32-row items
+    ([2500], 8, 8, True),                # G = 1: 128-row items
+    ([900], 40, 8, True),                # G = 5
+    ([1500], 32, 2, True),               # G = 16
+    ([1800, 40, 1], 16, 8, False),       # non-causal
+])
+def test_prefill_range_cut_items_vs_fp32(gpu, lens, hq, hkv, causal):
+    """The range schedule (four-wave workgroups, given a workspace, fewer
+    items than resident workgroups) cuts items across workgroups; their
+    partial softmax states meet in the workspace.  The output matches the fp32 closed form, every call leaves
+    the tickets at zero, and repeated calls give the same bits whichever
+    part arrives last -- also with the partial-state slots filled with NaN
+    before each call, so a part that folded a slot before its owner's saves
+    landed would show."""
+    from qwen3_engine_from_scratch_amd import _lib
+
+    lib = _lib.load()
+    c = oi.make_prefill_case(lens, hq, hkv, 128, seed=sum(lens) % 97)
+    tickets, slots = _layout(lib)
+    ws = torch.zeros(int(lib.qwen3_varlen_prefill_workspace_bytes()), dtype=torch.uint8,
+                     device=gpu)
+    announce(f"prefill range lens={lens} hq={hq} hkv={hkv} causal={causal}")
+    first = _call(lib, gpu, c, hq, hkv, ws, causal)
+    assert ws[slots:].any(), "no item was cut"
+    assert not ws[tickets].any(), "range tickets not left at zero"
+    assert_close_attn(first.cpu(), _gpu_ref_fp32(c, gpu, hq // hkv, causal), f"range lens={lens}")
+    for _ in range(3):
+        ws[slots:].fill_(0xFF)  # NaN in every float of every slot
+        again = _call(lib, gpu, c, hq, hkv, ws, causal)
+        assert torch.equal(again, first), "range output depends on the arrival order"
+        assert not ws[tickets].any()
+
+
+def test_prefill_range_matches_whole_items_when_uncut(gpu):
+    """Items the range schedule does not cut (here: a batch of short
+    prompts, at most four key tiles each) are computed exactly as the
+    persistent grid computes whole items (no workspace): the same bits."""
+    from qwen3_engine_from_scratch_amd import _lib
+
+    lib = _lib.load()
+    lens = [256, 17, 200, 131, 64, 1, 99, 250]
+    c = oi.make_prefill_case(lens, 16, 8, 128, seed=11)
+    ws = torch.zeros(int(lib.qwen3_varlen_prefill_workspace_bytes()), dtype=torch.uint8,
+                     device=gpu)
+    announce(f"prefill range vs whole items, {len(lens)} short prompts")
+    assert torch.equal(_call(lib, gpu, c, 16, 8, ws), _call(lib, gpu, c, 16, 8, None))
+
+
+def test_prefill_short_prompts_batch_invariant(gpu):
+    """A prompt of at most 256 tokens gives the same bits alone and inside a
+    larger batch (its items are never cut), as the reference's one program
+    per query block does."""
+    from qwen3_engine_from_scratch_amd import _lib
+
     lib = _lib.load()
     ws = torch.zeros(int(lib.qwen3_varlen_prefill_workspace_bytes()), dtype=torch.uint8,
                      device=gpu)
-
-    def call():
-        out = torch.empty_like(q)
-        rc = lib.qwen3_varlen_prefill_bf16(
-            q.data_ptr(), _lib.strides(q, (0, 1)), k.data_ptr(), _lib.strides(k, (0, 1)),
-            v.data_ptr(), _lib.strides(v, (0, 1)), out.data_ptr(), _lib.strides(out, (0, 1)),
-            cu.data_ptr(), len(lens), max(lens), q.shape[0], hq, hkv, 128, c.scale, 1,
-            ws.data_ptr(), ws.numel(), _lib.stream_of(gpu))
-        _lib.check(rc, "qwen3_varlen_prefill_bf16")
-        torch.cuda.synchronize()
-        return out
-
-    announce(f"prefill split items lens={lens} hq={hq} hkv={hkv}")
-    first = call()
-    assert ws[SPLIT_BUF:].any(), "no item was split"
-    assert not ws[SPLIT_CTR].any(), "split tickets / flags not left at zero"
-    assert_close_attn(first.cpu(), _gpu_ref_fp32(c, gpu, hq // hkv), f"split lens={lens}")
-    for _ in range(3):
-        assert torch.equal(call(), first), "split output depends on the arrival order"
-        assert not ws[SPLIT_CTR].any()
+    big = oi.make_prefill_case([2048, 256, 1000, 130, 77], 16, 8, 128, seed=12)
+    announce("prefill short prompts alone vs in a batch")
+    both = _call(lib, gpu, big, 16, 8, ws)
+    for s in (1, 3, 4):
+        s0, s1 = int(big.cu_seqlens[s]), int(big.cu_seqlens[s + 1])
+        alone = SimpleNamespace(q=big.q[s0:s1], k=big.k[s0:s1], v=big.v[s0:s1],
+                                cu_seqlens=torch.tensor([0, s1 - s0], dtype=torch.int32),
+                                lens=[s1 - s0], scale=big.scale)
+        assert torch.equal(_call(lib, gpu, alone, 16, 8, ws), both[s0:s1]), f"sequence {s}"
 
 
 def test_prefill_max_seqlen_is_an_upper_bound(gpu):
