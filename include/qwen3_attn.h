@@ -118,6 +118,49 @@ int qwen3_paged_decode_bf16(const void* q, const int64_t q_strides[2],
                             void* workspace, size_t workspace_bytes,
                             void* stream);
 
+/* Batch-invariant variant of qwen3_paged_decode_bf16: the same arguments and
+ * attention, computed so that a sequence's output bits depend only on its
+ * own q, K, V and length, never on the batch around it (the same alone, at
+ * any batch size, at any row position; the engine's batched == serial
+ * guarantee).  No counterpart in the reference, whose Triton kernel splits
+ * by batch shape; its callers are serving loops that need reproducible
+ * tokens whatever else is batched.
+ *   Each sequence-head is cut into 256-token partitions from its first
+ *   token; each partition's softmax state is computed on its own (16-token
+ *   tiles in pairs, from its first tile), and the output is the left fold of
+ *   the partition states in ascending order.  The batch only decides which
+ *   wave owns which partitions; a sequence split across waves is handed on
+ *   through the workspace with tickets (no wave waits for another).
+ *   workspace  qwen3_paged_decode_invariant_workspace_bytes() bytes, 16-byte
+ *              aligned: first the hand-off tickets (4 x 2048 x num_kv_heads
+ *              bytes, rounded up to 256), which must be zero before the
+ *              first call (every call leaves them zero; calls that share a
+ *              workspace use one num_kv_heads and one stream), then one slot
+ *              per 256-token partition of every (b, KV head) at the table's
+ *              full row length (B x num_kv_heads x ceil(max_pages x
+ *              block_size / 256) slots of G x (128 + 2) floats), plus
+ *              4 x (B + 1) + 256 bytes.  Depends on the launch shape only.
+ *   Launches the attention pass on `stream`, plus a merge kernel when a
+ *   table row can hold more than 32 partitions (8,192 tokens) or B > 2048.
+ * Costs more HBM time than qwen3_paged_decode_bf16 where sequences are
+ * split across waves (partition states written and read back). */
+size_t qwen3_paged_decode_invariant_workspace_bytes(int B, int num_heads, int num_kv_heads,
+                                                    int head_dim, int64_t max_pages,
+                                                    int block_size);
+int qwen3_paged_decode_invariant_bf16(const void* q, const int64_t q_strides[2],
+                                      const void* k_cache, const int64_t k_strides[3],
+                                      const void* v_cache, const int64_t v_strides[3],
+                                      int64_t num_blocks,
+                                      const int32_t* block_table, int64_t bt_row_stride,
+                                      int64_t max_rows, int64_t max_pages,
+                                      const int32_t* seq_lens, int seq_len_bias,
+                                      const int32_t* row_ids,
+                                      void* out, const int64_t out_strides[2],
+                                      int B, int num_heads, int num_kv_heads, int head_dim,
+                                      int block_size, float scale,
+                                      void* workspace, size_t workspace_bytes,
+                                      void* stream);
+
 /* Allocation-free variant of qwen3_paged_decode_bf16.  No counterpart in the
  * reference: it is for callers that cannot allocate device memory (code
  * under HIP graph capture, tight serving loops, harnesses that forbid

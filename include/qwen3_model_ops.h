@@ -184,7 +184,8 @@ int qwen3_sample_bf16(const void* logits, int64_t row_stride, int64_t rows, int6
  * a caller workspace of qwen3_sample_workspace_bytes(rows, vocab) bytes
  * (device, 16-byte aligned, no initialisation; calls that share one must
  * not overlap); 0 bytes means one part per row, and then, or with a NULL
- * workspace, this call is qwen3_sample_bf16. */
+ * workspace, this call is qwen3_sample_bf16.  A smaller workspace returns
+ * QWEN3_EWORKSPACE with the size needed in the error message. */
 size_t qwen3_sample_workspace_bytes(int64_t rows, int64_t vocab);
 int qwen3_sample_ws_bf16(const void* logits, int64_t row_stride, int64_t rows, int64_t vocab,
                          const float* temperature, const int32_t* top_k, const float* top_p,

@@ -35,6 +35,17 @@ _SIGNATURES = {
          _i, _i, _i, _i, _i, ctypes.c_float,
          _vp, ctypes.c_size_t, _vp],
     ),
+    "qwen3_paged_decode_invariant_workspace_bytes": (ctypes.c_size_t,
+                                                     [_i, _i, _i, _i, _i64, _i]),
+    "qwen3_paged_decode_invariant_bf16": (
+        _i,
+        [_vp, _c_i64p, _vp, _c_i64p, _vp, _c_i64p, _i64,
+         _vp, _i64, _i64, _i64,
+         _vp, _i, _vp,
+         _vp, _c_i64p,
+         _i, _i, _i, _i, _i, ctypes.c_float,
+         _vp, ctypes.c_size_t, _vp],
+    ),
     "qwen3_paged_decode_noalloc_bf16": (
         _i,
         [_vp, _c_i64p, _vp, _c_i64p, _vp, _c_i64p, _i64,
@@ -115,7 +126,7 @@ _SIGNATURES = {
     ),
 }
 
-ABI_VERSION = 8
+ABI_VERSION = 9
 
 _lib = None
 

@@ -36,4 +36,4 @@ int launch_status(const char* what) {
 
 extern "C" const char* qwen3_attn_last_error(void) { return q3::g_last_error; }
 
-extern "C" int qwen3_attn_abi_version(void) { return 8; }
+extern "C" int qwen3_attn_abi_version(void) { return 9; }

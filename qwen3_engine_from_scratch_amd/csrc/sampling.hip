@@ -1279,7 +1279,7 @@ extern "C" int qwen3_sample_ws_bf16(const void* logits, int64_t row_stride, int6
     return q3::fail(QWEN3_EINVAL, "%s: bad sizes", who);
   const size_t need = qwen3_sample_workspace_bytes(rows, vocab);
   if (workspace_bytes < need)
-    return q3::fail(QWEN3_EINVAL, "%s: workspace of %zu bytes, %zu needed", who,
+    return q3::fail(QWEN3_EWORKSPACE, "%s: workspace of %zu bytes, %zu needed", who,
                     workspace_bytes, need);
   if (!q3::aligned16(workspace))
     return q3::fail(QWEN3_EALIGN, "%s: workspace must be 16-byte aligned", who);

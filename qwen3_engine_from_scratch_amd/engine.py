@@ -66,10 +66,20 @@ class GenRequest:
 
 
 class Engine:
-    def __init__(self, model, pool, max_batch: int = 64, use_graph: bool = True):
+    def __init__(self, model, pool, max_batch: int = 64, use_graph: bool = True,
+                 batch_invariant: bool = False, max_prefill_batch: int | None = None):
+        """batch_invariant: decode attention on the batch-invariant kernel,
+        so a request's decode tokens do not depend on what else is batched
+        with it.  max_prefill_batch: prompts per prefill step (None: as many
+        as there are free rows); 1 prefills every prompt alone, as a
+        request running by itself would be (the library GEMMs of the
+        prefill pick kernels by row count, so a prompt's prefill bits depend
+        on the rows batched with it)."""
         self.model = model
         self.pool = pool
         self.max_batch = max_batch
+        self.max_prefill_batch = max_prefill_batch
+        model.decode_batch_invariant = batch_invariant
         self.device = pool.k_buffer.device
         self.runner = None
         self._placeholders = []
@@ -204,8 +214,10 @@ class Engine:
             ts = time.perf_counter()
             if waiting and len(running) < self.max_batch:
                 self._drain()
-                take = [waiting.popleft()
-                        for _ in range(min(self.max_batch - len(running), len(waiting)))]
+                n_take = min(self.max_batch - len(running), len(waiting))
+                if self.max_prefill_batch:
+                    n_take = min(n_take, self.max_prefill_batch)
+                take = [waiting.popleft() for _ in range(n_take)]
                 self._prefill(take)
                 running.extend(take)
                 prefill_s += time.perf_counter() - ts

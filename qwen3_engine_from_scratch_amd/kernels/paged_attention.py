@@ -29,20 +29,48 @@ __all__ = [
 ]
 
 
+_INV_WORKSPACES: dict = {}
+# Workspaces replaced by a larger one stay allocated: a graph captured
+# earlier holds the old address and may still be replayed.
+_SUPERSEDED: list = []
+
+
+def _invariant_workspace(dev, stream: int, num_kv_heads: int, need: int) -> torch.Tensor:
+    """The batch-invariant decode's workspace kept for this device, stream and
+    KV-head count, grown as needed, zeroed when allocated (its hand-off
+    tickets start at zero and every call leaves them there).  One per stream:
+    calls on different streams may run at the same time and must not share
+    tickets."""
+    key = (str(dev), stream, num_kv_heads)
+    ws = _INV_WORKSPACES.get(key)
+    if ws is None or ws.numel() < need:
+        if ws is not None:
+            _SUPERSEDED.append(ws)
+        ws = torch.zeros(max(need, 1), dtype=torch.uint8, device=dev)
+        _INV_WORKSPACES[key] = ws
+    return ws
+
+
 def paged_decode_workspace_bytes(batch: int, num_heads: int, num_kv_heads: int, head_dim: int,
-                                 max_pages: int, block_size: int) -> int:
-    """Split-KV workspace size on the current device; depends only on the
-    launch shape, so a graph captured once stays valid for any live context
-    lengths."""
-    return int(_lib.load().qwen3_paged_decode_workspace_bytes(
-        batch, num_heads, num_kv_heads, head_dim, max_pages, block_size))
+                                 max_pages: int, block_size: int, *,
+                                 batch_invariant: bool = False) -> int:
+    """Workspace size of the decode on the current device; depends only on
+    the launch shape, so a graph captured once stays valid for any live
+    context lengths.  batch_invariant: the size for the batch-invariant
+    kernel (one slot per 256-token partition of every (row, KV head) at the
+    table's full row length, after the hand-off tickets)."""
+    lib = _lib.load()
+    fn = (lib.qwen3_paged_decode_invariant_workspace_bytes if batch_invariant
+          else lib.qwen3_paged_decode_workspace_bytes)
+    return int(fn(batch, num_heads, num_kv_heads, head_dim, max_pages, block_size))
 
 
 def paged_attention_decode_hip(q, k_buffer, v_buffer, block_table_2d,
                                seq_lens_full, row_ids, block_size, *,
                                seq_len_bias: int = 1, scale: float | None = None,
                                out: torch.Tensor | None = None,
-                               workspace: torch.Tensor | None = None):
+                               workspace: torch.Tensor | None = None,
+                               batch_invariant: bool = False):
     """Bare kernel entry (reference: paged_attention_decode_triton,
     qwen3/kernels/paged_attention.py:132-178).
 
@@ -57,6 +85,14 @@ def paged_attention_decode_hip(q, k_buffer, v_buffer, block_table_2d,
     seq_lens_full[row] + seq_len_bias tokens (bias 1 = the reference's
     convention, :55).  The softmax scale is 1/sqrt(head_dim) as the reference
     recomputes it (:161) unless `scale` is given.
+
+    batch_invariant: use the batch-invariant kernel (each sequence's output
+    bits independent of the rest of the batch; qwen3_attn.h).  `workspace`:
+    paged_decode_workspace_bytes(..., batch_invariant=...) bytes; for the
+    batch-invariant kernel its leading ticket region must be zero before its
+    first call (every call leaves it zero).  Default: a fresh one per call
+    (default kernel) or one per device, stream and KV-head count kept by this
+    module (batch-invariant kernel).
     """
     B, num_heads, head_dim = q.shape
     num_blocks, num_kv_heads, block_size_check, head_dim_check = k_buffer.shape
@@ -86,11 +122,15 @@ def paged_attention_decode_hip(q, k_buffer, v_buffer, block_table_2d,
         _lib.require_hip(out)
     max_rows, max_pages = block_table_2d.shape
     need = paged_decode_workspace_bytes(B, num_heads, num_kv_heads, head_dim, max_pages,
-                                        block_size)
+                                        block_size, batch_invariant=batch_invariant)
     if workspace is None or workspace.numel() < need:
-        workspace = torch.empty(max(need, 1), dtype=torch.uint8, device=dev)
+        if batch_invariant:
+            workspace = _invariant_workspace(dev, _lib.stream_of(dev), num_kv_heads, need)
+        else:
+            workspace = torch.empty(max(need, 1), dtype=torch.uint8, device=dev)
     lib = _lib.load()
-    rc = lib.qwen3_paged_decode_bf16(
+    fn = lib.qwen3_paged_decode_invariant_bf16 if batch_invariant else lib.qwen3_paged_decode_bf16
+    rc = fn(
         q.data_ptr(), _lib.strides(q, (0, 1)),
         k_buffer.data_ptr(), _lib.strides(k_buffer, (0, 1, 2)),
         v_buffer.data_ptr(), _lib.strides(v_buffer, (0, 1, 2)),
@@ -100,7 +140,8 @@ def paged_attention_decode_hip(q, k_buffer, v_buffer, block_table_2d,
         out.data_ptr(), _lib.strides(out, (0, 1)),
         B, num_heads, num_kv_heads, head_dim, block_size, float(scale),
         workspace.data_ptr(), workspace.numel(), _lib.stream_of(dev))
-    _lib.check(rc, "qwen3_paged_decode_bf16")
+    _lib.check(rc, "qwen3_paged_decode_invariant_bf16" if batch_invariant
+               else "qwen3_paged_decode_bf16")
     return out
 
 

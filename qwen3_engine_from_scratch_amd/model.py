@@ -134,8 +134,14 @@ class Qwen3ForCausalLM(nn.Module):
         self.lm_head = nn.Linear(config.hidden_size, config.vocab_size, bias=False)
         if config.tie_word_embeddings:
             self.lm_head.weight = self.model.embed_tokens.weight
-        self._workspace = None
+        self._workspace = None       # decode attention workspace of the current mode
+        self._ws_mode = None
+        self._superseded = []
         self._head_ws = None
+        # Decode attention with the batch-invariant kernel: each sequence's
+        # tokens independent of the rest of the batch (batched == serial),
+        # at some HBM time where sequences are split across waves.
+        self.decode_batch_invariant = False
 
     # ---- shared layer loop -------------------------------------------------
 
@@ -165,15 +171,23 @@ class Qwen3ForCausalLM(nn.Module):
     # ---- decode ------------------------------------------------------------
 
     def reserve_decode_workspace(self, batch: int, pool) -> None:
-        """Allocates the split-KV workspace of the decode attention for up to
-        `batch` rows once (a captured graph keeps using it)."""
+        """Allocates the workspace of the decode attention (in the current
+        mode, decode_batch_invariant) for up to `batch` rows once (a captured
+        graph keeps using it)."""
+        inv = bool(self.decode_batch_invariant)
         need = paged_decode_workspace_bytes(batch, self.config.num_attention_heads,
                                             self.config.num_key_value_heads,
                                             self.config.head_dim, pool.block_table_2d.shape[1],
-                                            pool.block_size)
-        if self._workspace is None or self._workspace.numel() < need:
-            self._workspace = torch.empty(max(need, 1), dtype=torch.uint8,
+                                            pool.block_size, batch_invariant=inv)
+        if self._workspace is None or self._ws_mode != inv or self._workspace.numel() < need:
+            if self._workspace is not None:
+                # a graph captured earlier may still replay on the old buffer
+                self._superseded.append(self._workspace)
+            # zeroed once: the batch-invariant kernel's hand-off tickets start
+            # at zero and every call leaves them there
+            self._workspace = torch.zeros(max(need, 1), dtype=torch.uint8,
                                           device=pool.k_buffer.device)
+            self._ws_mode = inv
         if self._head_ws is None:
             self._head_ws = torch.empty(int(_lib.load().qwen3_lm_head_argmax_workspace_bytes()),
                                         dtype=torch.uint8, device=pool.k_buffer.device)
@@ -219,7 +233,8 @@ class Qwen3ForCausalLM(nn.Module):
                                 i, row_ids, positions)
             o = paged_attention_decode_hip(q, pool.k_buffer[:, i], pool.v_buffer[:, i],
                                            pool.block_table_2d, pool.seq_lens, row_ids,
-                                           pool.block_size, workspace=ws)
+                                           pool.block_size, workspace=ws,
+                                           batch_invariant=self._ws_mode)
             decode_linear(o.view(B, Hq * D), at.o_proj.weight, epilogue="residual",
                           residual=h_a, residual_out=h_b, ss_out=ss_b)
             act = decode_linear(h_b, layer.mlp.gate_up_proj.weight, epilogue="silu", ss_in=ss_b,
@@ -279,7 +294,8 @@ class Qwen3ForCausalLM(nn.Module):
                                      positions=positions)
             o = paged_attention_decode_hip(qr, pool.k_buffer[:, i], pool.v_buffer[:, i],
                                            pool.block_table_2d, pool.seq_lens, row_ids,
-                                           pool.block_size)
+                                           pool.block_size, workspace=ws,
+                                           batch_invariant=self._ws_mode)
             return o.view(B, Hq * D)
 
         if fused is None:

@@ -54,12 +54,15 @@ def _all_greedy(temperature) -> bool:
 
 
 _WORKSPACES: dict = {}
+# Workspaces replaced by a larger one stay allocated until the process ends:
+# a graph captured earlier holds the old address and may still be replayed.
+_SUPERSEDED: list = []
 
 
 def _workspace(dev, stream: int, B: int, V: int):
     """The parallel form's workspace for this device and stream (grown, never
-    shrunk); None under graph capture when it would have to grow (the call
-    then takes the single-workgroup form, which needs none)."""
+    shrunk, never freed); None under graph capture when it would have to grow
+    (the call then takes the single-workgroup form, which needs none)."""
     need = int(_lib.load().qwen3_sample_workspace_bytes(B, V))
     if need == 0:  # one part per row: the single-workgroup form
         return None
@@ -69,6 +72,8 @@ def _workspace(dev, stream: int, B: int, V: int):
         return ws
     if torch.cuda.is_current_stream_capturing():
         return None
+    if ws is not None:
+        _SUPERSEDED.append(ws)
     ws = torch.empty(need, dtype=torch.uint8, device=dev)
     _WORKSPACES[key] = ws
     return ws

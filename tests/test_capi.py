@@ -60,6 +60,20 @@ def test_workspace_bytes():
     slots = 4096 * 32 * -(-512 * 16 // 2048)
     assert lib.qwen3_paged_decode_workspace_bytes(4096, 32, 8, 128, 512, 16) == \
         a256(slots * 128 * 4) + a256(slots * 4)
+    # the batch-invariant decode: tickets for 2048 rows x KV heads, then one
+    # slot per (b, KV head, 256-token partition) of a full table row (G x 128
+    # floats of output, G (max, denominator) pairs), the (B + 1)-entry tile
+    # prefix and the tiles-per-wave word; the same on any device
+    for B, hq, hkv, pages in ((256, 32, 8, 512), (256, 16, 8, 512), (256, 16, 1, 512),
+                              (4096, 32, 8, 512), (3, 32, 8, 17)):
+        G = hq // hkv
+        slots = B * hkv * -(-pages * 16 // 256)
+        expect = (a256(2048 * hkv * 4) + a256(slots * G * 128 * 4) + a256(slots * G * 8)
+                  + a256((B + 1) * 4) + 256)
+        assert lib.qwen3_paged_decode_invariant_workspace_bytes(B, hq, hkv, 128, pages, 16) == expect
+    assert lib.qwen3_paged_decode_invariant_workspace_bytes(2, 32, 8, 128, 8, 64) == \
+        65536 + a256(2 * 8 * 2 * 4 * 512) + a256(2 * 8 * 2 * 4 * 8) + 256 + 256  # 2 parts
+    assert lib.qwen3_paged_decode_invariant_workspace_bytes(4, 16, 3, 128, 64, 16) == 0
     assert lib.qwen3_paged_decode_workspace_bytes(4, 16, 8, 64, 64, 16) == 0  # head_dim 64 not built
     assert lib.qwen3_paged_decode_workspace_bytes(4, 16, 8, 128, 64, 8) == 0  # block_size 8
     assert lib.qwen3_paged_decode_workspace_bytes(4, 16, 3, 128, 64, 16) == 0  # 16 % 3 != 0
@@ -188,7 +202,7 @@ def test_model_ops_reject_bad_arguments():
     assert int(lib.qwen3_sample_workspace_bytes(1, 1000)) == 0      # one round: one part
     assert int(lib.qwen3_sample_workspace_bytes(1, 20000)) == 1 * 3 * 32784  # three rounds
     assert lib.qwen3_sample_ws_bf16(FAKE, 151936, 64, 151936, None, None, None, 1, FAKE,
-                                    FAKE, need - 16, None) == -1  # workspace too small
+                                    FAKE, need - 16, None) == -4  # workspace too small
     assert lib.qwen3_sample_ws_bf16(FAKE, 151936, 64, 151936, None, None, None, 1, FAKE,
                                     FAKE + 8, need, None) == -2   # misaligned workspace
     assert lib.qwen3_sample_ws_bf16(FAKE, 100, 4, 151936, None, None, None, 1, FAKE,

@@ -569,3 +569,31 @@ def test_engine_greedy_generation_vs_oracle(gpu):
         assert out[-1] == eos or len(out) == n
         stopped += out[-1] == eos and len(out) < n
     assert stopped >= 1, "no request stopped at eos"
+
+
+def test_engine_graph_equals_eager_batch_invariant(gpu):
+    """With the batch-invariant decode attention every kernel of a decode
+    step is row-invariant, so the captured engine (padded power-of-two
+    buckets with dummy rows) and the eager engine (unpadded batches) give
+    the same tokens, token for token."""
+    from qwen3_engine_from_scratch_amd.engine import Engine, GenRequest
+
+    model, state, cfg = _tiny(seed=4)
+    model = model.to(gpu)
+    g = torch.Generator().manual_seed(11)
+    lens = [5, 63, 17, 40, 1, 33]
+    new = [12, 3, 20, 7, 9, 1]
+    prompts = [torch.randint(0, cfg.vocab_size, (L,), generator=g).tolist() for L in lens]
+    results = {}
+    for use_graph in (True, False):
+        pool = _pool(cfg, gpu, blocks=128, max_requests=32)
+        announce(f"engine batch_invariant use_graph={use_graph}, max_batch=4")
+        eng = Engine(model, pool, max_batch=4, use_graph=use_graph, batch_invariant=True)
+        reqs = [GenRequest(i, p, n) for i, (p, n) in enumerate(zip(prompts, new))]
+        eng.generate(reqs)
+        eng.close()
+        assert pool.free_count == pool.total_blocks, "pages not returned"
+        results[use_graph] = [r.output_ids for r in reqs]
+    model.decode_batch_invariant = False
+    for i, (x, y) in enumerate(zip(results[True], results[False])):
+        assert x == y, f"request {i}: graph and eager engines differ: {x} vs {y}"

@@ -28,7 +28,7 @@ from oracle import model as om
 
 pytestmark = pytest.mark.gpu
 
-N_PROMPTS, CAP, NEW = 20, 160, 10
+N_PROMPTS, CAP, NEW = 40, 160, 10
 
 
 @pytest.fixture(scope="module")
@@ -102,19 +102,24 @@ def test_qwen3_0p6b_teacher_forced_logits_vs_oracle(gpu, qwen3_0p6b):
 
 
 def test_qwen3_0p6b_engine_greedy_vs_oracle(gpu, qwen3_0p6b):
-    """Continuous batching through captured graphs (buckets up to 64; 20
-    requests run in the 32-row bucket, so the decode linears take their
-    above-16-row path), greedy tokens checked against the fp32 oracle."""
+    """Continuous batching through captured graphs (buckets up to 64; 40
+    requests run in the 64-row bucket: a 64-row captured step, the 64-row
+    gate/up kernel and a 64-sequence paged decode), greedy tokens checked
+    against the fp32 oracle."""
     from qwen3_engine_from_scratch_amd.engine import Engine, GenRequest
 
     model, state, cfg, prompts = qwen3_0p6b
     pool = _pool(cfg, gpu, N_PROMPTS, CAP + NEW + 8, graph_rows=64)
     announce(f"Qwen3-0.6B engine: {N_PROMPTS} requests, prompts <= {CAP}, {NEW} greedy tokens")
     eng = Engine(model, pool, max_batch=64, use_graph=True)
+    buckets = []
+    bucket_for = eng.runner.bucket_for
+    eng.runner.bucket_for = lambda k: buckets.append(bucket_for(k)) or buckets[-1]
     reqs = [GenRequest(i, p, NEW) for i, p in enumerate(prompts)]
     st = eng.generate(reqs)
     eng.close()
     assert st["output_tokens"] == N_PROMPTS * NEW
+    assert buckets and set(buckets) == {64}, buckets
     assert pool.free_count == pool.total_blocks, "pages not returned"
     agree = total = 0
     worst = 0.0
