@@ -19,9 +19,13 @@ Also reported on the same line:
   cpu_baseline  the oracle's restatement of the reference's PyTorch decode path
                 (qwen3/paged_attention.py:39-122) on the host cores, over a
                 bounded sample (the first 64 sequences) of the same workload;
+  decode_long_context  the same decode over 8 contexts in [32768, 131072];
+  decode_batch_invariant  both decode workloads on the batch-invariant
+                kernel (each sequence's output bits independent of the batch);
   prefill       varlen causal prefill at the Qwen3-0.6B shape (8 sequences,
                 lengths uniform in [64, 2048], 16/8 heads) in TFLOP/s against
-                the 2.5 PFLOP/s bf16 dense MFMA peak, plus its slot write;
+                the 2.5 PFLOP/s bf16 dense MFMA peak, plus its slot write and
+                a single 2,048-token prompt;
   pre_attention the fused QK-RMSNorm + RoPE + pool write (prefill and decode
                 forms) against the HBM peak;
   sampling      greedy and top-k / top-p token sampling over a 64 x 151936
@@ -321,7 +325,7 @@ def workload_lengths(name: str) -> list:
     return seeded_lengths(*WORKLOAD_LENGTHS[name])
 
 
-def bench_decode(args, dev):
+def bench_decode(args, dev, batch_invariant=False):
     import torch
 
     from qwen3_engine_from_scratch_amd.kernels.paged_attention import (
@@ -337,12 +341,14 @@ def bench_decode(args, dev):
     log(f"decode inputs: B={len(lens)} sumL={sum(lens)}")
     t = decode_inputs(lens, hq, hkv, dev)
     out = torch.empty_like(t["q"])
-    ws = torch.empty(paged_decode_workspace_bytes(len(lens), hq, hkv, 128, t["bt"].shape[1], 16),
+    # zeroed: the batch-invariant kernel's tickets start at zero
+    ws = torch.zeros(paged_decode_workspace_bytes(len(lens), hq, hkv, 128, t["bt"].shape[1], 16,
+                                                  batch_invariant=batch_invariant),
                      dtype=torch.uint8, device=dev)
 
     def step():
         paged_attention_decode_hip(t["q"], t["k"], t["v"], t["bt"], t["seq_lens"], t["row_ids"],
-                                   16, out=out, workspace=ws)
+                                   16, out=out, workspace=ws, batch_invariant=batch_invariant)
 
     wall_ms, evt_ms = time_steps(step, args.steps, args.warmup)
     nbytes = decode_bytes(lens, hq, hkv)
@@ -714,9 +720,40 @@ def bench_prefill(args, dev):
                           "GB/s_back_to_back": round(wbytes / (w_hot * 1e-3) / 1e9, 1),
                           "copy_same_bytes": copy_reference(wbytes, dev, args.steps,
                                                             args.warmup)}}
+    res["single_2048"] = bench_prefill_single(args, dev)
     if not args.no_cpu_baseline:
         res["cpu_baseline"] = cpu_baseline_prefill(lens, q, k, v, flops)
     return res
+
+
+def bench_prefill_single(args, dev, L=2048):
+    """One causal prompt of L tokens (Qwen3-0.6B heads): the small-batch case
+    of the prefill, where the range schedule cuts the longest query tiles'
+    items across workgroups; back-to-back graph replays, HIP events."""
+    import torch
+
+    from qwen3_engine_from_scratch_amd.kernels.flash_attention_varlen import flash_attention_prefill
+
+    g = torch.Generator(device=dev).manual_seed(1)
+    q = torch.randn(L, 16, 128, device=dev, generator=g).to(torch.bfloat16)
+    k = torch.randn(L, 8, 128, device=dev, generator=g).to(torch.bfloat16)
+    v = torch.randn(L, 8, 128, device=dev, generator=g).to(torch.bfloat16)
+    cu = torch.tensor([0, L], dtype=torch.int32, device=dev)
+    out = torch.empty_like(q)
+
+    def step():
+        flash_attention_prefill(q, k, v, cu, 128 ** -0.5, 16, 8, 128, max_seqlen=L, out=out)
+
+    warm_up(step)
+    evt_ms = time_graph(step, args.steps, args.warmup)
+    flops = 2 * 128 * 16 * L * (L + 1)
+    tflops = flops / (evt_ms * 1e-3) / 1e12
+    log(f"prefill single {L}-token prompt: {evt_ms * 1e3:.1f} us/call, {tflops:.1f} TFLOP/s")
+    return {"workload": f"varlen causal prefill, one {L}-token prompt, 16/8 heads, head_dim 128, "
+                        "bf16", "value": round(tflops, 2), "unit": "TFLOP/s",
+            "ms_per_step": round(evt_ms, 5), "flops": flops,
+            "frac_mfma_peak": round(tflops / MFMA_BF16_PEAK_TFLOPS, 4),
+            "timing": "graph replay of back-to-back calls, HIP events"}
 
 
 def cpu_baseline_prefill(lens, q, k, v, flops, reps=3):
@@ -899,6 +936,8 @@ def main(argv=None):
                     help="prefill line: the Qwen3-0.6B ragged causal batch, or 8 x 4096 tokens "
                          "non-causal (steady-state rate; profiling only, with --only prefill)")
     ap.add_argument("--cpu-sample", type=int, default=64, help="sequences in the CPU baseline sample")
+    ap.add_argument("--no-invariant", action="store_true",
+                    help="skip the batch-invariant decode lines")
     ap.add_argument("--no-long-context", action="store_true",
                     help="skip the secondary long-context (B=8, up to 128k tokens) decode line")
     ap.add_argument("--calibrate-copy", action="store_true",
@@ -966,6 +1005,18 @@ def main(argv=None):
                 "frac_hbm_peak": round(r4["bytes"] / (r4["evt_ms"] * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)}
             del r4
             torch.cuda.empty_cache()
+        if args.workload == "config3" and not args.no_invariant:
+            for wl in ("config3", "config4"):
+                ri = bench_decode(argparse.Namespace(**{**vars(args), "workload": wl}), dev,
+                                  batch_invariant=True)
+                gb = ri["bytes"] / (ri["evt_ms"] * 1e-3) / 1e9
+                line.setdefault("decode_batch_invariant", {})[wl] = {
+                    "workload": ri["wname"] + " on qwen3_paged_decode_invariant_bf16 (each "
+                                "sequence's bits independent of the batch)",
+                    "value": round(gb, 1), "unit": "GB/s", "ms_per_step": round(ri["evt_ms"], 5),
+                    "frac_hbm_peak": round(gb / HBM_PEAK_GBS, 4)}
+                del ri
+                torch.cuda.empty_cache()
     if args.only in (None, "config1"):
         line["decode_config1"] = bench_decode_config1(args, dev)
         if args.only == "config1":

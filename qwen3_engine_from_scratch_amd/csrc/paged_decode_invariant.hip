@@ -3,11 +3,14 @@
 // that a sequence's output bits depend only on its own query, K/V and
 // length, never on the batch around it.
 //
-//  * Every sequence-head is cut into canonical partitions of kPartTiles
-//    tiles (256 tokens) from its first tile.  A partition's softmax state
-//    starts fresh and folds its tiles in load batches of kChunk from its
-//    first tile; the output is the left fold of the partition states in
-//    ascending order, with one fold formula everywhere.
+//  * Every sequence-head is cut into canonical partitions from its first
+//    tile: 16 tiles (256 tokens), or 32 tiles (512 tokens) for
+//    sequence-heads of 4,096 tokens or more (fewer hand-offs where they are
+//    long; the size depends on the sequence's own length only).  A
+//    partition's softmax state starts fresh and folds its tiles in load
+//    batches of kChunk from its first tile; the output is the left fold of
+//    the partition states in ascending order, with one fold formula
+//    everywhere.
 //  * The batch only decides which wave owns which partitions (persistent
 //    waves over the flat tile list, as in the default path, with ranges
 //    rounded to partition starts), so work stays balanced to within one
@@ -23,13 +26,18 @@
 
 namespace {
 
-// Tiles of one canonical partition of a sequence-head (256 tokens): the
-// unit of work a wave owns, and of the merge.
-constexpr int kPartTiles = 16;
+// Tiles of one canonical partition of a sequence-head of n tiles: the unit
+// of work a wave owns, and of the merge.
+constexpr int kPartTiles = 16;       // the smallest (slots are sized for it)
+constexpr int kLongPartTiles = 32;
+constexpr int kLongTiles = 256;      // from 4,096 tokens on
+__host__ __device__ constexpr int part_tiles(int n) {
+  return n >= kLongTiles ? kLongPartTiles : kPartTiles;
+}
 
 // ---------------------------------------------------------------------------
 // Canonical partitions.  Every sequence-head is cut into partitions of
-// kPartTiles tiles from its first tile; a partition's softmax state starts
+// part_tiles(n) tiles from its first tile; a partition's softmax state starts
 // fresh and folds its tiles in load batches of kChunk tiles from its first
 // tile, and the output is the left fold of the partition states in
 // ascending partition order.  Both launch paths and the merge compute
@@ -129,16 +137,17 @@ struct Split {
 
 __device__ __forceinline__ Split split_of(int64_t S, int n, int64_t pw) {
   Split s;
-  s.k = (n + kPartTiles - 1) / kPartTiles;
+  const int P = part_tiles(n);
+  s.k = (n + P - 1) / P;
   const int64_t w0 = S / pw;
-  if (kPartTiles > pw) {  // every partition starts in another wave's range
+  if (P > pw) {  // every partition starts in another wave's range
     s.N = s.k;
     s.j1 = 1;
     return s;
   }
-  s.N = static_cast<int>((S + static_cast<int64_t>(s.k - 1) * kPartTiles) / pw - w0 + 1);
+  s.N = static_cast<int>((S + static_cast<int64_t>(s.k - 1) * P) / pw - w0 + 1);
   const int64_t x = (w0 + 1) * pw - S;
-  s.j1 = x >= n ? s.k : static_cast<int>((x + kPartTiles - 1) / kPartTiles);
+  s.j1 = x >= n ? s.k : static_cast<int>((x + P - 1) / P);
   return s;
 }
 
@@ -240,8 +249,9 @@ void paged_decode_inv_stream_kernel(DecodeArgs a) {
     const int n = pref(b + 1) - pref(b);
     const int64_t off = g - static_cast<int64_t>(a.Hkv) * pref(b);
     const int64_t start = g - off % n;  // first tile of the sequence-head
-    const int64_t j = q3::cdiv(off % n, kPartTiles);
-    return j * kPartTiles >= n ? start + n : start + j * kPartTiles;
+    const int P = part_tiles(n);
+    const int64_t j = q3::cdiv(off % n, P);
+    return j * P >= n ? start + n : start + j * P;
   };
   // The wave owns the partitions whose first tile lies in [w*pw, (w+1)*pw).
   const int64_t g0 = part_align(w * pw);
@@ -306,6 +316,7 @@ void paged_decode_inv_stream_kernel(DecodeArgs a) {
 
   // ---- compute side ----
   int cseg = -1, cb = 0, chkv = 0, cn = 0, pstart = 0, ct_hi = 0, seg_hi = 0;
+  int cP = kPartTiles;  // partition tiles of the sequence-head
   bool own = false;       // the segment starts at the sequence-head's first tile
   bool complete = false;  // the segment ends at its last tile
   bool emit = false;      // each partition state goes to its slot
@@ -428,12 +439,12 @@ void paged_decode_inv_stream_kernel(DecodeArgs a) {
   // the segment's end the output is written or the part is handed on.
   // Runs after the batch's math, while its registers are free.
   auto end_batch = [&]() __attribute__((always_inline)) {
-    if (ct_hi != seg_hi && ct_hi % kPartTiles != 0) return;
+    if (ct_hi != seg_hi && ct_hi % cP != 0) return;
     st.l = q3::sum_xor32(q3::sum_xor16(st.l));
     const bool last = ct_hi == seg_hi;
     if (emit) {
       state_to_lds();
-      lds_to_slot(static_cast<int64_t>(cseg) * a.max_parts + pstart / kPartTiles);
+      lds_to_slot(static_cast<int64_t>(cseg) * a.max_parts + pstart / cP);
     } else if (!have_f) {
       if (last && complete) {  // a whole sequence-head of one partition
         const float inv = st.l > 0.f ? 1.f / st.l : 0.f;
@@ -477,6 +488,7 @@ void paged_decode_inv_stream_kernel(DecodeArgs a) {
     cb = c.seg / a.Hkv;
     chkv = c.seg % a.Hkv;
     cn = c.ntiles;
+    cP = part_tiles(cn);
     const int64_t cS = static_cast<int64_t>(a.Hkv) * pref(cb) + static_cast<int64_t>(chkv) * cn;
     seg_hi = g1 - cS < cn ? static_cast<int>(g1 - cS) : cn;
     own = c.t0 == 0;
@@ -487,7 +499,7 @@ void paged_decode_inv_stream_kernel(DecodeArgs a) {
     if (!(own && complete)) sp = split_of(cS, cn, pw);
     if (!own) {
       emit = true;
-      const int ja = c.t0 / kPartTiles;  // this part's first partition
+      const int ja = c.t0 / cP;  // this part's first partition
       if (complete && ja - sp.j1 + 1 <= kInlineSlots) {
         // the last part: when every other part is in, fold them first
         uint32_t t = 0;
@@ -564,7 +576,8 @@ void paged_decode_inv_grid_kernel(DecodeArgs a) {
   const int64_t row = row_of(a, b);
   const int L = static_cast<int>(row >= 0 ? clamp_len(a, a.seq_lens[row]) : 0);
   const int n_tiles = static_cast<int>(q3::cdiv(L, kTile));
-  const int t0 = j * kPartTiles;
+  const int P = part_tiles(n_tiles);
+  const int t0 = j * P;
   if (t0 >= n_tiles) {
     if (j == 0) {  // empty context: defined zero output
       for (int e = lane; e < G * kD; e += 64) {
@@ -574,8 +587,8 @@ void paged_decode_inv_grid_kernel(DecodeArgs a) {
     }
     return;
   }
-  const int t1 = min(n_tiles, t0 + kPartTiles);
-  // A partition spans at most kPartTiles * kTile / block_size <= kWin pages.
+  const int t1 = min(n_tiles, t0 + P);
+  // A partition spans at most kLongPartTiles * kTile / block_size <= kWin pages.
   const int base = (t0 * kTile) / a.bs;
   const int32_t pages = table_entry(a, row, base + lane);
   const uint16_t* kbase = a.k + static_cast<int64_t>(hkv) * a.k_sh;
@@ -619,7 +632,7 @@ void paged_decode_inv_grid_kernel(DecodeArgs a) {
     issue(cbuf);
   }
   st.l = q3::sum_xor32(q3::sum_xor16(st.l));
-  if (n_tiles <= kPartTiles) {  // the only partition: the output itself
+  if (n_tiles <= P) {  // the only partition: the output itself
     const float inv = st.l > 0.f ? 1.f / st.l : 0.f;
     if (lo < G) store_out_bf16(a, b, hkv * G + lo, st.acc, inv, hi);
   } else {
@@ -647,7 +660,7 @@ __global__ __launch_bounds__(kMaxG * 64) void paged_decode_inv_merge_kernel(Deco
   if (a.grid_mode) {
     const int64_t row = row_of(a, b);
     n = static_cast<int>(q3::cdiv(row >= 0 ? clamp_len(a, a.seq_lens[row]) : 0, kTile));
-    todo = n > kPartTiles;
+    todo = n > part_tiles(n);
   } else {
     todo = a.tickets[static_cast<int64_t>(b) * a.Hkv + hkv] == kMergeLater;
     if (todo) {
@@ -658,7 +671,7 @@ __global__ __launch_bounds__(kMaxG * 64) void paged_decode_inv_merge_kernel(Deco
     }
   }
   if (todo) {
-    const int k = static_cast<int>(q3::cdiv(n, kPartTiles));
+    const int k = static_cast<int>(q3::cdiv(n, part_tiles(n)));
     const int64_t hq = static_cast<int64_t>(hkv) * G + g;
     const int64_t s0 = slot_of(a, b, hkv, 0);
     auto acc_at = [&](int j) {
