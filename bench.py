@@ -337,6 +337,8 @@ def bench_decode(args, dev, batch_invariant=False):
     else:
         lens, wname = workload_lengths("config3"), ("paged decode attention, Qwen3-8B shape: "
                                                     "B=256, L~U[1024,8192]")
+    if batch_invariant:
+        wname += " on the batch-invariant kernel (qwen3_paged_decode_invariant_bf16)"
     hq, hkv = 32, 8
     log(f"decode inputs: B={len(lens)} sumL={sum(lens)}")
     t = decode_inputs(lens, hq, hkv, dev)
@@ -938,6 +940,9 @@ def main(argv=None):
     ap.add_argument("--cpu-sample", type=int, default=64, help="sequences in the CPU baseline sample")
     ap.add_argument("--no-invariant", action="store_true",
                     help="skip the batch-invariant decode lines")
+    ap.add_argument("--decode-kernel", choices=["default", "invariant"], default="default",
+                    help="kernel of the headline decode line (invariant: the batch-invariant "
+                         "one, without the extra decode lines)")
     ap.add_argument("--no-long-context", action="store_true",
                     help="skip the secondary long-context (B=8, up to 128k tokens) decode line")
     ap.add_argument("--calibrate-copy", action="store_true",
@@ -971,7 +976,8 @@ def main(argv=None):
             "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "bf16",
             "data": "synthetic (seeded N(0,1) q/K/V, seeded lengths and block tables)"}
     if args.only in (None, "decode"):
-        res = bench_decode(args, dev)
+        inv_main = args.decode_kernel == "invariant"
+        res = bench_decode(args, dev, batch_invariant=inv_main)
         gbs = res["bytes"] / (res["wall_ms"] * 1e-3) / 1e9
         ach = res["bytes"] / (res["evt_ms"] * 1e-3) / 1e9
         line.update(value=round(gbs, 1), unit="GB/s", ms_per_step=round(res["wall_ms"], 5))
@@ -979,12 +985,15 @@ def main(argv=None):
                           "block 16, pool 1.1x pages, random-permutation block tables",
                           "batch": len(res["lens"]), "sum_context_tokens": sum(res["lens"]),
                           "bytes_per_step": res["bytes"]}
-        traffic = profiled_traffic(TRAFFIC_PROFILE) if args.workload == "config3" else None
+        traffic = (profiled_traffic(TRAFFIC_PROFILE) if args.workload == "config3" and not inv_main
+                   else None)
         line["roofline"] = {"bound": "hbm", "achieved": round(ach, 1), "peak": HBM_PEAK_GBS,
                             "unit": "GB/s", "frac": round(ach / HBM_PEAK_GBS, 4),
                             "traffic": traffic, "kernel_ms": round(res["evt_ms"], 5),
-                            "kernel": "paged_decode_stream_kernel + paged_decode_stream_merge_kernel "
-                                      "(one decode call), HIP events on the launch stream",
+                            "kernel": ("paged_decode_inv_stream_kernel (+ paged_decode_inv_merge_"
+                                       "kernel when launched)" if inv_main else
+                                       "paged_decode_stream_kernel + paged_decode_stream_merge_kernel")
+                                      + " (one decode call), HIP events on the launch stream",
                             "traffic_source": f"profiles/{TRAFFIC_PROFILE}" if traffic else None}
         if not args.no_cpu_baseline:
             line["cpu_baseline"] = cpu_baseline_decode(res, args.cpu_sample)
@@ -995,7 +1004,7 @@ def main(argv=None):
         line["roofline"]["stream_read_reference"] = stream_read_reference(nbytes, dev)
         line["roofline"]["frac_of_stream_read"] = round(
             line["roofline"]["achieved"] / line["roofline"]["stream_read_reference"]["GB/s"], 4)
-        if args.workload == "config3" and not args.no_long_context:
+        if args.workload == "config3" and not args.no_long_context and not inv_main:
             long_args = argparse.Namespace(**{**vars(args), "workload": "config4"})
             r4 = bench_decode(long_args, dev)
             line["decode_long_context"] = {
@@ -1005,14 +1014,13 @@ def main(argv=None):
                 "frac_hbm_peak": round(r4["bytes"] / (r4["evt_ms"] * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)}
             del r4
             torch.cuda.empty_cache()
-        if args.workload == "config3" and not args.no_invariant:
+        if args.workload == "config3" and not args.no_invariant and not inv_main:
             for wl in ("config3", "config4"):
                 ri = bench_decode(argparse.Namespace(**{**vars(args), "workload": wl}), dev,
                                   batch_invariant=True)
                 gb = ri["bytes"] / (ri["evt_ms"] * 1e-3) / 1e9
                 line.setdefault("decode_batch_invariant", {})[wl] = {
-                    "workload": ri["wname"] + " on qwen3_paged_decode_invariant_bf16 (each "
-                                "sequence's bits independent of the batch)",
+                    "workload": ri["wname"] + ": each sequence's bits independent of the batch",
                     "value": round(gb, 1), "unit": "GB/s", "ms_per_step": round(ri["evt_ms"], 5),
                     "frac_hbm_peak": round(gb / HBM_PEAK_GBS, 4)}
                 del ri
