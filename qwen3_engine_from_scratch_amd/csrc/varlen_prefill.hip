@@ -36,10 +36,18 @@
 //    each weighted by its cost plus a fixed cost per item, are laid end to
 //    end and cut into equal ranges, one per resident workgroup.  A
 //    workgroup streams its range as a chain of segments (runs of one
-//    item's key tiles): the next segment's first K/V tile and Q rows load
-//    during the current segment's last tile.  An item whose tiles fall in
-//    several ranges leaves one partial softmax state per range in the
-//    workspace; the last part to arrive folds them in key order.
+//    item's key tiles), each starting with the loads of its first K/V tile
+//    and its Q rows.  An item whose tiles fall in several ranges leaves one
+//    partial softmax state per range in the workspace; the last part to
+//    arrive folds them in key order.
+//  * Wave-specialised tile (varlen_prefill_ws_kernel, QWEN3_PREFILL_TILE=ws):
+//    matrix waves issue only MFMAs, softmax waves turn scores into P^T
+//    operands, both through LDS; it moves 1.75 times the LDS bytes per MFMA
+//    of the tile above and runs slower (LDS-bound), so it is not the
+//    default.
+#include <cstdlib>
+#include <cstring>
+
 #include "common.hpp"
 
 namespace {
@@ -121,8 +129,8 @@ struct TileBufs {
 struct LaneOffsets {
   uint32_t kdma[kMaxDma];  // source offset of this lane's K chunk, load j
   uint32_t vdma[kMaxDma];  // same for V
-  uint32_t kread[8];           // LDS offset of the QK operand, d step t (key block 0)
-  uint32_t vread[4];           // LDS offset of the PV operand, d block db (key chunk 0)
+  uint32_t kread;              // LDS offset of the QK operand, d step 0 (key block 0)
+  uint32_t vread;              // LDS offset of the PV operand, d block 0 (key chunk 0)
 };
 
 template <int W>
@@ -140,20 +148,19 @@ __device__ __forceinline__ LaneOffsets lane_offsets(int lane, int wave, int64_t 
     o.kdma[j] = static_cast<uint32_t>(row * k_row_bytes) + ((slot ^ (row & 15)) << 4);
     o.vdma[j] = static_cast<uint32_t>(row * v_row_bytes) + ((slot ^ (4 * (row & 3))) << 4);
   }
-  // QK A operand (mfma 32x32x16): lane reads key row lane % 32, chunk 2t + lane / 32.
+  // QK A operand (mfma 32x32x16): lane reads key row lane % 32, chunk 2t + lane / 32
+  // at chunk (2t + h) ^ (r % 16) = (h ^ (r % 16)) ^ 2t: d step t is kread ^ (t << 5)
+  // (the XOR stays inside the row's 256 bytes).
   const int r = lane & 31, h = lane >> 5;
-#pragma unroll
-  for (int t = 0; t < 8; ++t) o.kread[t] = r * kRowBytes + ((((2 * t) | h) ^ (r & 15)) << 4);
+  o.kread = r * kRowBytes + ((h ^ (r & 15)) << 4);
   // PV A operand (V^T) through ds_read_b64_tr_b16: in 16-lane group g, lane
   // m supplies row 4 (g / 2) + m / 4 (+ 8 for the second read, + 16 per key
   // chunk) and dims 32 db + 16 (g % 2) + 4 (m % 4) .. +3.
+  // Slot 4 (db ^ (m / 4)) + ..: d block db is vread ^ (db << 6).
   const int g = lane >> 4, m = lane & 15;
   const int vrow = 4 * (g >> 1) + (m >> 2);
-#pragma unroll
-  for (int db = 0; db < 4; ++db) {
-    const int slot = 4 * (db ^ (m >> 2)) + 2 * (g & 1) + ((m & 3) >> 1);
-    o.vread[db] = vrow * kRowBytes + slot * 16 + 8 * (m & 1);
-  }
+  const int slot = 4 * (m >> 2) + 2 * (g & 1) + ((m & 3) >> 1);
+  o.vread = vrow * kRowBytes + slot * 16 + 8 * (m & 1);
   return o;
 }
 
@@ -202,12 +209,12 @@ constexpr int kAhead = 2;
 
 // Byte offset of the K operand of QK step u (key block u % 2, d step u / 2).
 __device__ __forceinline__ uint32_t qk_operand(const LaneOffsets& off, int u) {
-  return off.kread[u >> 1] + (u & 1) * 32 * kRowBytes;
+  return (off.kread ^ static_cast<uint32_t>((u >> 1) << 5)) + (u & 1) * 32 * kRowBytes;
 }
 
 // Byte offset of the V^T operand of PV step u (key chunk u / 4, d block u % 4).
 __device__ __forceinline__ uint32_t pv_operand(const LaneOffsets& off, int u) {
-  return off.vread[u & 3] + (u >> 2) * 16 * kRowBytes;
+  return (off.vread ^ static_cast<uint32_t>((u & 3) << 6)) + (u >> 2) * 16 * kRowBytes;
 }
 
 // Maximum of the 32 scores s[0..1][0..15] of one lane: four interleaved
@@ -552,6 +559,245 @@ void varlen_prefill_flat_kernel(PrefillArgs a) {
   const int64_t end = a.cu[seq + 1];
   if (start < 0 || end > a.total || end <= start) return;
   prefill_item<W>(a, off, start, static_cast<int>(end - start), hg, mt, tb);
+}
+
+// ---------------------------------------------------------------------------
+// Wave-specialised tile (varlen_prefill_ws_kernel): one 768-thread workgroup
+// per CU, four matrix waves and eight softmax waves, so each SIMD holds one
+// matrix wave and the two softmax waves that serve it.  A matrix wave owns
+// 32 query rows (Q and the O^T accumulator in registers) and issues only the
+// MFMA products; each of its two softmax waves owns 16 of those query
+// columns (their running max and sum) and turns the fp32 scores into bf16
+// P^T operands.  Scores and P go through LDS, in a three-stage pipeline
+// with one barrier per phase: in phase k the matrix waves run QK of tile k
+// and PV of tile k - 2, the softmax waves the softmax of tile k - 1 and the
+// loads of K(k + 1) and V(k - 1).
+//
+// LDS (160 KiB, all of it): K and V double buffers (4 x 16 KiB), scores
+// (2 x 4 x 8 KiB: [32 queries][64 keys] fp32 per matrix wave, 16-byte chunk
+// c of row q at c ^ (q % 16)), P^T operands (2 x 4 x 4 KiB: [4 key chunks]
+// [64 lanes] x 16 B per matrix wave).  A softmax wave's rescale factor of
+// query q goes into float 2 q of row q of the score buffer it has just read
+// (the matrix wave reads it before it writes that buffer again; 32 rows on
+// 32 distinct banks), its final sum into float 2 q + 1 after the last phase.
+constexpr int kWsMatrix = 4;
+constexpr int kWsSoft = 8;
+constexpr int kWsWaves = kWsMatrix + kWsSoft;
+
+// Loads one K or V tile of this softmax wave's share (eight waves, two
+// 16-byte loads each per lane) into dst.
+__device__ __forceinline__ void ws_dma(const uint16_t* base, int64_t row_st, int rows,
+                                       const uint32_t (&offs)[kMaxDma], uint16_t* dst, int si) {
+  const int bytes = static_cast<int>((rows - 1) * row_st * 2) + kRowBytes;
+  const __amdgpu_buffer_rsrc_t r =
+      __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t*>(base), 0, bytes, 0x00020000);
+  constexpr int D = dma_per_wave<8>();
+#pragma unroll
+  for (int j = 0; j < D; ++j)
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (lds_void_t*)(dst + (D * si + j) * 512), 16,
+                                             offs[j], 0, 0, 0);
+}
+
+// Maximum of 16 scores (v_max3 chains; fmaxf would canonicalize each input).
+__device__ __forceinline__ float max3_16(const q3::f32x4 (&x)[4]) {
+  float m, t;
+  asm volatile(
+      "v_max3_f32 %0, %2, %3, %4\n\t"
+      "v_max3_f32 %1, %10, %11, %12\n\t"
+      "v_max3_f32 %0, %0, %5, %6\n\t"
+      "v_max3_f32 %1, %1, %13, %14\n\t"
+      "v_max3_f32 %0, %0, %7, %8\n\t"
+      "v_max3_f32 %1, %1, %15, %16\n\t"
+      "v_max3_f32 %0, %0, %9, %17\n\t"
+      "v_max_f32 %0, %0, %1"
+      : "=&v"(m), "=&v"(t)
+      : "v"(x[0][0]), "v"(x[0][1]), "v"(x[0][2]), "v"(x[0][3]), "v"(x[1][0]), "v"(x[1][1]),
+        "v"(x[1][2]), "v"(x[1][3]), "v"(x[2][0]), "v"(x[2][1]), "v"(x[2][2]), "v"(x[2][3]),
+        "v"(x[3][0]), "v"(x[3][1]), "v"(x[3][2]), "v"(x[3][3]));
+  return m;
+}
+
+__global__ __launch_bounds__(kWsWaves * 64) __attribute__((amdgpu_waves_per_eu(3, 3)))
+void varlen_prefill_ws_kernel(PrefillArgs a) {
+  __shared__ __attribute__((aligned(1024))) uint16_t s_k0[kTileElems];
+  __shared__ __attribute__((aligned(1024))) uint16_t s_k1[kTileElems];
+  __shared__ __attribute__((aligned(1024))) uint16_t s_v0[kTileElems];
+  __shared__ __attribute__((aligned(1024))) uint16_t s_v1[kTileElems];
+  __shared__ __attribute__((aligned(1024))) float s_sc[2][kWsMatrix][32 * kBN];
+  __shared__ __attribute__((aligned(1024))) q3::u32x4 s_pt[2][kWsMatrix][4 * 64];
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  // the item: as the flat grid of four-wave workgroups
+  const int64_t id = blockIdx.x;
+  const int hg = static_cast<int>(id % a.groups);
+  const int seq = static_cast<int>((id / a.groups) % a.num_seqs);
+  const int mt =
+      a.n_mtiles - 1 - static_cast<int>(id / (static_cast<int64_t>(a.groups) * a.num_seqs));
+  const int64_t start = a.cu[seq];
+  const int64_t end = a.cu[seq + 1];
+  if (start < 0 || end > a.total || end <= start) return;
+  const int len = static_cast<int>(end - start);
+  if (mt * a.rows >= len) return;
+  const int kend = a.causal ? min(len, mt * a.rows + a.rows) : len;
+  const int n = (kend + kBN - 1) / kBN;
+  const float c = a.scale_log2;
+  const bool matrix = wave < kWsMatrix;
+  const int si = wave - kWsMatrix;                 // softmax wave index
+  const int mi = matrix ? wave : si >> 1;          // the matrix wave served
+  const WaveItem wi = wave_item<4>(a, start, len, hg, mt, mi, lane);
+  const uint16_t* kb = a.k + start * a.k_st + static_cast<int64_t>(wi.kvh) * a.k_sh;
+  const uint16_t* vb = a.v + start * a.v_st + static_cast<int64_t>(wi.kvh) * a.v_sh;
+  auto kbuf = [&](int i) { return i ? s_k1 : s_k0; };
+  auto vbuf = [&](int i) { return i ? s_v1 : s_v0; };
+
+  if (matrix) {
+    // ---------------- matrix wave ----------------
+    const LaneOffsets off = lane_offsets<4>(lane, 0, a.k_st * 2, a.v_st * 2);
+    const int q = lane & 31;
+    q3::bf16x8 qv[8];
+    load_q(a, wi, q_lane_offset(a, lane), qv);
+    q3::f32x16 acc[4];
+#pragma unroll
+    for (int db = 0; db < 4; ++db)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) acc[db][r] = 0.f;
+    wait_loads();
+    __syncthreads();  // K(0) staged
+    for (int k = 0; k < n + 2; ++k) {
+      const bool qk = k < n, pv = k >= 2;
+      const int b = k & 1;  // buffers of tile k (K, scores) and of tile k - 2 (V, scores, P)
+      float* sc = s_sc[b][mi];
+      if (pv) {  // the softmax waves' rescale of tile k - 2, read before S(k) overwrites it
+        const float alpha = sc[q * kBN + 2 * q];
+        if (__any(alpha != 1.f)) {
+#pragma unroll
+          for (int db = 0; db < 4; ++db) acc[db] *= alpha;
+        }
+      }
+      if (qk) {
+        const uint16_t* kt = kbuf(b);
+        q3::f32x16 s[2];
+#pragma unroll
+        for (int kb2 = 0; kb2 < 2; ++kb2)
+#pragma unroll
+          for (int r = 0; r < 16; ++r) s[kb2][r] = 0.f;
+        q3::bf16x8 kf[kAhead];
+#pragma unroll
+        for (int u = 0; u < kAhead; ++u) kf[u] = lds_ld16(kt, qk_operand(off, u));
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int u = 0; u < 16; ++u) {
+          s[u & 1] = q3::mfma32x32x16(kf[u % kAhead], qv[u >> 1], s[u & 1]);
+          if (u + kAhead < 16) kf[u % kAhead] = lds_ld16(kt, qk_operand(off, u + kAhead));
+          __builtin_amdgcn_sched_barrier(0);
+        }
+        // S^T -> the score buffer: lane (q, hl) holds keys 32 kb2 + 8 j + 4 hl
+        // + 0..3 in s[kb2][4 j .. 4 j + 3], chunk 8 kb2 + 2 j + hl of row q.
+        const int hl = lane >> 5;
+#pragma unroll
+        for (int kb2 = 0; kb2 < 2; ++kb2)
+#pragma unroll
+          for (int j = 0; j < 4; ++j) {
+            const int ch = 8 * kb2 + 2 * j + hl;
+            *reinterpret_cast<q3::f32x4*>(sc + q * kBN + 4 * (ch ^ (q & 15))) =
+                q3::f32x4{s[kb2][4 * j], s[kb2][4 * j + 1], s[kb2][4 * j + 2], s[kb2][4 * j + 3]};
+          }
+      }
+      if (pv) {
+        const uint16_t* vt = vbuf(b);
+        const q3::u32x4* pt = s_pt[b][mi];
+        q3::bf16x8 vf[kAhead];
+        q3::bf16x8 pf[2];  // P^T operand of key chunk u / 4, one chunk ahead
+        pf[0] = q3::as_bf16x8(pt[lane]);
+#pragma unroll
+        for (int u = 0; u < kAhead; ++u) vf[u] = lds_vt(vt, pv_operand(off, u));
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int u = 0; u < 16; ++u) {
+          if ((u & 3) == 0 && u + 4 < 16) pf[((u >> 2) + 1) & 1] = q3::as_bf16x8(pt[(u >> 2) * 64 + 64 + lane]);
+          acc[u & 3] = q3::mfma32x32x16(vf[u % kAhead], pf[(u >> 2) & 1], acc[u & 3]);
+          if (u + kAhead < 16) vf[u % kAhead] = lds_vt(vt, pv_operand(off, u + kAhead));
+          __builtin_amdgcn_sched_barrier(0);
+        }
+      }
+      wait_loads();
+      __syncthreads();
+    }
+    __syncthreads();  // the softmax waves' final sums are in
+    const float l = s_sc[0][mi][q * kBN + 2 * q + 1];
+    if (!wi.active()) return;
+    // staging: this wave's half of a K buffer (no reads or loads of it remain)
+    char* stage = reinterpret_cast<char*>(mi < 2 ? s_k0 : s_k1) + (mi & 1) * 8192;
+    store_output(a, wi, lane, o_lane_offset(a, lane), l, acc, stage);
+    return;
+  }
+  // ---------------- softmax wave ----------------
+  const LaneOffsets off8 = lane_offsets<8>(lane, si, a.k_st * 2, a.v_st * 2);
+  const int ql = lane & 15, g = lane >> 4;
+  const int qm = 16 * (si & 1) + ql;  // query column within the matrix wave
+  float m_run = q3::kNegInf, l_run = 0.f;
+  ws_dma(kb, a.k_st, min(kBN, len), off8.kdma, s_k0, si);
+  wait_loads();
+  __syncthreads();  // K(0) staged
+  for (int k = 0; k < n + 2; ++k) {
+    if (k + 1 < n) {
+      const int n0 = (k + 1) * kBN;
+      ws_dma(kb + n0 * a.k_st, a.k_st, min(kBN, len - n0), off8.kdma, kbuf((k + 1) & 1), si);
+    }
+    if (k >= 1 && k - 1 < n) {
+      const int n0 = (k - 1) * kBN;
+      ws_dma(vb + n0 * a.v_st, a.v_st, min(kBN, len - n0), off8.vdma, vbuf((k - 1) & 1), si);
+    }
+    if (k >= 1 && k <= n) {
+      const int t = k - 1, b = t & 1, n0 = t * kBN;
+      float* sc = s_sc[b][mi];
+      q3::f32x4 x[4];  // keys n0 + 16 g + 4 i + e
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+        x[i] = *reinterpret_cast<const q3::f32x4*>(sc + qm * kBN + 4 * ((4 * g + i) ^ (qm & 15)));
+      const bool need_mask = (n0 + kBN > len) || (a.causal && n0 + kBN - 1 > wi.q0);
+      if (need_mask) {
+        int lim = len - 1 - n0 - 16 * g;
+        if (a.causal) lim = min(lim, wi.q0 + qm - n0 - 16 * g);
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+#pragma unroll
+          for (int e = 0; e < 4; ++e) x[i][e] = 4 * i + e <= lim ? x[i][e] : q3::kNegInf;
+      }
+      float bm = max3_16(x);
+      bm = q3::max_xor32(q3::max_xor16(bm));
+      const float m_cand = bm * c;
+      const bool raise = m_cand > m_run + kRescaleSlack;
+      const float m_new = raise ? m_cand : m_run;
+      const float alpha = raise ? q3::fast_exp2(m_run - m_new) : 1.f;
+      m_run = m_new;
+      const float m_use = m_run == q3::kNegInf ? 0.f : m_run;
+      float e[4][4];
+      float ps = 0.f;
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          e[i][j] = q3::fast_exp2(__builtin_fmaf(x[i][j], c, -m_use));
+          ps += e[i][j];
+        }
+      ps = q3::sum_xor32(q3::sum_xor16(ps));
+      l_run = __builtin_fmaf(l_run, alpha, ps);
+      // P^T operands of key chunk g: lane slot qm + 32 hl holds keys
+      // 16 g + 4 hl + {0..3, 8..11}.
+      q3::u32x4* pt = s_pt[b][mi] + g * 64 + qm;
+      pt[0] = q3::u32x4{q3::pack_bf16x2(e[0][0], e[0][1]), q3::pack_bf16x2(e[0][2], e[0][3]),
+                        q3::pack_bf16x2(e[2][0], e[2][1]), q3::pack_bf16x2(e[2][2], e[2][3])};
+      pt[32] = q3::u32x4{q3::pack_bf16x2(e[1][0], e[1][1]), q3::pack_bf16x2(e[1][2], e[1][3]),
+                         q3::pack_bf16x2(e[3][0], e[3][1]), q3::pack_bf16x2(e[3][2], e[3][3])};
+      if (g == 0) sc[qm * kBN + 2 * qm] = alpha;  // read by the matrix wave before PV of this tile
+    }
+    wait_loads();
+    __syncthreads();
+  }
+  if (g == 0) s_sc[0][mi][qm * kBN + 2 * qm + 1] = l_run;
+  __syncthreads();
 }
 
 // Exclusive prefix sum over n <= kScanMax ints held in LDS (in place); returns
@@ -976,65 +1222,68 @@ __device__ __forceinline__ void save_partial(__amdgpu_buffer_rsrc_t slot, int wa
   __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(l_run), slot, ml + 4, 0, kCpolDevice);
 }
 
-// Folds a saved part into (m_run, l_run, acc): the state becomes relative
-// to the larger running max, state * 2^(m_state - m) + part * 2^(m_part - m).
-// Parts are folded in key order, so the bits depend only on the parts.  The
-// accumulators go in two halves of 32 (one memory round trip each).
-template <int W>
-__device__ __forceinline__ void fold_partial(__amdgpu_buffer_rsrc_t slot, int wave, int lane,
-                                             float& m_run, float& l_run, q3::f32x16 (&acc)[4]) {
-  const uint32_t ml = slot_ml_offset<W>() + (wave * 64 + lane) * 8;
-  const float om = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(slot, ml, 0, kCpolDevice));
-  const float ol =
-      __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(slot, ml + 4, 0, kCpolDevice));
-  const float m = fmaxf(m_run, om);
-  const float m_use = m == q3::kNegInf ? 0.f : m;
-  const float a_s = q3::fast_exp2(m_run - m_use);  // exp2(-inf) = 0: an empty side adds nothing
-  const float a_p = q3::fast_exp2(om - m_use);
-  m_run = m;
-  l_run = __builtin_fmaf(ol, a_p, l_run * a_s);
-#pragma unroll
-  for (int half = 0; half < 2; ++half) {
-    q3::f32x4 x[8];
-#pragma unroll
-    for (int i = 0; i < 8; ++i)
-      x[i] = __builtin_bit_cast(
-          q3::f32x4, __builtin_amdgcn_raw_buffer_load_b128(
-                         slot, static_cast<uint32_t>(((wave * 16 + 8 * half + i) * 64 + lane) * 16),
-                         0, kCpolDevice));
-#pragma unroll
-    for (int i = 0; i < 8; ++i)
-#pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        const int k = 8 * half + i;
-        const float y = acc[k >> 2][4 * (k & 3) + e];
-        acc[k >> 2][4 * (k & 3) + e] = __builtin_fmaf(x[i][e], a_p, y * a_s);
-      }
-  }
-}
+// One saved part of a cut item, as this lane holds it: the running max,
+// the sum and 16 x 4 accumulator floats.
+struct PartState {
+  float m, l;
+  q3::f32x4 x[16];
+};
 
+// Issues every load of a saved part at once (one memory round trip).
 template <int W>
-__device__ __forceinline__ void load_partial(__amdgpu_buffer_rsrc_t slot, int wave, int lane,
-                                             float& m_run, float& l_run, q3::f32x16 (&acc)[4]) {
+__device__ __forceinline__ PartState load_part(__amdgpu_buffer_rsrc_t slot, int wave, int lane) {
+  PartState st;
   const uint32_t ml = slot_ml_offset<W>() + (wave * 64 + lane) * 8;
-  m_run = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(slot, ml, 0, kCpolDevice));
-  l_run = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(slot, ml + 4, 0, kCpolDevice));
+  st.m = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(slot, ml, 0, kCpolDevice));
+  st.l = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(slot, ml + 4, 0, kCpolDevice));
 #pragma unroll
-  for (int i = 0; i < 16; ++i) {
-    const q3::f32x4 x = __builtin_bit_cast(
+  for (int i = 0; i < 16; ++i)
+    st.x[i] = __builtin_bit_cast(
         q3::f32x4, __builtin_amdgcn_raw_buffer_load_b128(
                        slot, static_cast<uint32_t>(((wave * 16 + i) * 64 + lane) * 16), 0,
                        kCpolDevice));
+  return st;
+}
+
+// Folds a part into (m_run, l_run, acc): the state becomes relative to the
+// larger running max, state * 2^(m_state - m) + part * 2^(m_part - m).
+// From the empty state (m_run = -inf, l_run = 0, acc = 0) the result is the
+// part itself (factors 0 and exp2(0) = 1).
+__device__ __forceinline__ void fold_state(const PartState& st, float& m_run, float& l_run,
+                                           q3::f32x16 (&acc)[4]) {
+  const float m = fmaxf(m_run, st.m);
+  const float m_use = m == q3::kNegInf ? 0.f : m;
+  const float a_s = q3::fast_exp2(m_run - m_use);  // exp2(-inf) = 0: an empty side adds nothing
+  const float a_p = q3::fast_exp2(st.m - m_use);
+  m_run = m;
+  l_run = __builtin_fmaf(st.l, a_p, l_run * a_s);
 #pragma unroll
-    for (int e = 0; e < 4; ++e) acc[i >> 2][4 * (i & 3) + e] = x[e];
-  }
+  for (int i = 0; i < 16; ++i)
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const float y = acc[i >> 2][4 * (i & 3) + e];
+      acc[i >> 2][4 * (i & 3) + e] = __builtin_fmaf(st.x[i][e], a_p, y * a_s);
+    }
+}
+
+// Folds parts p0 .. nseg - 1 of the cut item whose first range is vfirst
+// (part 0: slot 2 vfirst + 1, part p > 0: slot 2 (vfirst + p)), in key
+// order, so the bits depend only on the parts: one memory round trip per
+// part (two parts in flight would not fit the tile loop's registers).
+template <int W>
+__device__ __forceinline__ void fold_parts(const PrefillArgs& a, int vfirst, int p0, int nseg,
+                                           int wave, int lane, float& m_run, float& l_run,
+                                           q3::f32x16 (&acc)[4]) {
+  for (int p = p0; p < nseg; ++p)
+    fold_state(load_part<W>(slot_rsrc<W>(a, p == 0 ? 2 * vfirst + 1 : 2 * (vfirst + p)), wave,
+                            lane),
+               m_run, l_run, acc);
 }
 
 // Range grid (CUs x resident workgroups, a multiple of 8): range v of N
 // (ranges of workgroups on one XCD adjacent when every workgroup has one)
-// is streamed as a chain of segments.  The first K/V tile and the Q rows
-// of the next segment load during the current segment's last tile, so a
-// segment start costs no memory round trip.  A segment of a cut item
+// is streamed as a chain of segments, each starting with the loads of its
+// first K/V tile and its Q rows.  A segment of a cut item
 // saves its partial state in slot 2 v (the range's first segment) or
 // 2 v + 1 (its last, the part holding the item's tile 0), then takes the
 // item's ticket; the part taking the last ticket folds every part in key
@@ -1149,8 +1398,7 @@ void varlen_prefill_range_kernel(PrefillArgs a) {
         if (tid == 0) s_ticket = __hip_atomic_load(ticket, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         __syncthreads();
         if (s_ticket == last) {  // every other part has saved: fold them in without saving
-          for (int p = 1; p < nseg; ++p)
-            fold_partial<W>(slot_rsrc<W>(a, 2 * (vfirst + p)), wave, lane, m_run, l_run, acc);
+          fold_parts<W>(a, vfirst, 1, nseg, wave, lane, m_run, l_run, acc);
           merged = true;
         }
         __syncthreads();  // s_ticket is reused below
@@ -1164,9 +1412,13 @@ void varlen_prefill_range_kernel(PrefillArgs a) {
           s_ticket = __hip_atomic_fetch_add(ticket, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         __syncthreads();
         if (s_ticket == last) {  // the last part in: fold all saved parts, in key order
-          load_partial<W>(slot_rsrc<W>(a, 2 * vfirst + 1), wave, lane, m_run, l_run, acc);
-          for (int p = 1; p < nseg; ++p)
-            fold_partial<W>(slot_rsrc<W>(a, 2 * (vfirst + p)), wave, lane, m_run, l_run, acc);
+          m_run = q3::kNegInf;
+          l_run = 0.f;
+#pragma unroll
+          for (int db = 0; db < 4; ++db)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) acc[db][r] = 0.f;
+          fold_parts<W>(a, vfirst, 0, nseg, wave, lane, m_run, l_run, acc);
           merged = true;
         }
       }
@@ -1180,6 +1432,14 @@ void varlen_prefill_range_kernel(PrefillArgs a) {
     }
     __syncthreads();  // the staging buffers are read before the next segment's loads refill them
   }
+}
+
+// QWEN3_PREFILL_TILE=ws selects the wave-specialised tile (flat grid of
+// four-wave items) for batches that would take the four-wave path; read at
+// every call.
+bool ws_tile_selected() {
+  const char* e = std::getenv("QWEN3_PREFILL_TILE");
+  return e && std::strcmp(e, "ws") == 0;
 }
 
 // Resident workgroups per CU of a kernel, queried once per device (a
@@ -1356,6 +1616,17 @@ extern "C" int qwen3_varlen_prefill_bf16(const void* q, const int64_t q_strides[
     a.tickets = reinterpret_cast<uint32_t*>(ws + kCtrBytes);
     a.slots = reinterpret_cast<float*>(ws + kCtrBytes + ticket_bytes(n));
     a.max_ranges = static_cast<int>(n);
+  }
+  if (ws_tile_selected()) {  // flat grid of four-wave items on the wave-specialised tile
+    a.rows = 32 * 4 / a.HG;
+    a.n_mtiles = static_cast<int>(q3::cdiv(max_seqlen, a.rows));
+    const int64_t blocks = static_cast<int64_t>(a.groups) * num_seqs * a.n_mtiles;
+    if (blocks > 0x7fffffff)
+      return q3::fail(QWEN3_EINVAL, "%s: grid too large (heads %d, seqs %d, max_seqlen %d)", who,
+                      a.Hq, num_seqs, max_seqlen);
+    hipLaunchKernelGGL(varlen_prefill_ws_kernel, dim3(static_cast<unsigned>(blocks)),
+                       dim3(kWsWaves * 64), 0, s, a);
+    return q3::launch_status(who);
   }
   return wide ? launch_prefill<8>(a, num_seqs, max_seqlen, dev, cus, s, who)
               : launch_prefill<4>(a, num_seqs, max_seqlen, dev, cus, s, who);
