@@ -318,7 +318,12 @@ __device__ __forceinline__ void load_q(const PrefillArgs& a, const WaveItem& wi,
 }
 
 // One 64-key tile (first key n0, staged in kt / vt) folded into this wave's
-// online softmax state.
+// online softmax state.  Prio: the wave runs its two MFMA chains at raised
+// issue priority, so of the two waves on a SIMD the one feeding the matrix
+// core issues first (measured: 1 µs faster on one 2,048-token prompt in the
+// range schedule, 3-4 µs slower on the Qwen3-0.6B batch in the persistent
+// one, so only the range schedule sets it).
+template <bool Prio>
 __device__ __forceinline__ void tile_math(const PrefillArgs& a, const LaneOffsets& off,
                                           const WaveItem& wi, int lane, int n0,
                                           const uint16_t* kt, const uint16_t* vt,
@@ -343,12 +348,14 @@ __device__ __forceinline__ void tile_math(const PrefillArgs& a, const LaneOffset
 #pragma unroll
     for (int u = 0; u < kAhead; ++u) kf[u] = lds_ld16(kt, qk_operand(off, u));
     __builtin_amdgcn_sched_barrier(0);
+    if constexpr (Prio) __builtin_amdgcn_s_setprio(1);
 #pragma unroll
     for (int u = 0; u < 16; ++u) {
       s[u & 1] = q3::mfma32x32x16(kf[u % kAhead], qv[u >> 1], s[u & 1]);
       if (u + kAhead < 16) kf[u % kAhead] = lds_ld16(kt, qk_operand(off, u + kAhead));
       __builtin_amdgcn_sched_barrier(0);
     }
+    if constexpr (Prio) __builtin_amdgcn_s_setprio(0);
   }
   // ---- mask (diagonal / tail tiles only) and block max ----
   const bool need_mask = (n0 + kBN > wi.len) || (a.causal && n0 + kBN - 1 > wi.q0);
@@ -412,6 +419,7 @@ __device__ __forceinline__ void tile_math(const PrefillArgs& a, const LaneOffset
 #pragma unroll
   for (int h = 0; h < 4; ++h) exp_pair(0, h);
   __builtin_amdgcn_sched_barrier(0);
+  if constexpr (Prio) __builtin_amdgcn_s_setprio(1);
 #pragma unroll
   for (int u = 0; u < 16; ++u) {
     acc[u & 3] = q3::mfma32x32x16(vf[u % kAhead], q3::as_bf16x8(pk[u >> 2]), acc[u & 3]);
@@ -419,6 +427,7 @@ __device__ __forceinline__ void tile_math(const PrefillArgs& a, const LaneOffset
     if (u < 12) exp_pair((u >> 2) + 1, u & 3);
     __builtin_amdgcn_sched_barrier(0);
   }
+  if constexpr (Prio) __builtin_amdgcn_s_setprio(0);
   l_run += (psum[0] + psum[1]) + (psum[2] + psum[3]);
 }
 
@@ -475,7 +484,7 @@ __device__ __forceinline__ void store_output(const PrefillArgs& a, const WaveIte
 // tile's loads are issued before the previous tile's math (two buffer
 // pairs, one barrier per tile).  Every thread of the workgroup calls it;
 // all four tile buffers are free when it returns.
-template <int W>
+template <int W, bool Prio = false>
 __device__ __forceinline__ void run_tiles(const PrefillArgs& a, const LaneOffsets& off,
                                           const WaveItem& wi, int t0, int t1, const TileBufs& tb,
                                           int lane, int wave, float& m_run, float& l_run,
@@ -493,7 +502,7 @@ __device__ __forceinline__ void run_tiles(const PrefillArgs& a, const LaneOffset
   __syncthreads();
   auto tile = [&](int it, const uint16_t* kt, const uint16_t* vt, uint16_t* nk, uint16_t* nv) {
     if (it + 1 < t1) tile_dma<W>(a, off, wi.start, wi.len, wi.kvh, (it + 1) * kBN, nk, nv, wave);
-    tile_math(a, off, wi, lane, it * kBN, kt, vt, qv, m_run, l_run, acc);
+    tile_math<Prio>(a, off, wi, lane, it * kBN, kt, vt, qv, m_run, l_run, acc);
     wait_loads();
     __syncthreads();
   };
@@ -1385,7 +1394,7 @@ void varlen_prefill_range_kernel(PrefillArgs a) {
     const WaveItem wi = wave_item<W>(a, cur.start, cur.len, cur.hg, cur.mt, wave, lane);
     float m_run, l_run;
     q3::f32x16 acc[4];  // acc[db][r] = O[q0 + l32][32*db + 8*(r/4) + 4*hl + r%4]
-    run_tiles<W>(a, off, wi, cur.j0, cur.j1, tb, lane, wave, m_run, l_run, acc);
+    run_tiles<W, true>(a, off, wi, cur.j0, cur.j1, tb, lane, wave, m_run, l_run, acc);
     bool write = !cur.cut;
     if (cur.cut) {
       int vfirst, nseg;
