@@ -131,3 +131,36 @@ def test_decode_invariant_workspace_contract(gpu, B, lo, hi):
         assert torch.equal(out, full[torch.tensor(rows, device=gpu)])
     ref = gpu_dense_decode_fp32(t["q"], t["k"], t["v"], t["bt"], t["seq_lens"], t["row_ids"], 16)
     assert_close_attn(full, ref, "invariant workspace contract")
+
+
+@pytest.mark.parametrize("hq,hkv,bs", [(8, 8, 16), (32, 4, 16), (32, 2, 32), (16, 8, 32)])
+def test_decode_invariant_group_sizes_and_blocks(gpu, hq, hkv, bs):
+    """G = 1, 8, 16 and 2 with 16- and 32-token blocks: lengths around the
+    256-token partitions, around 4,096 tokens (where partitions become 512
+    tokens) and a long one; values against the fp32 reference, every row
+    alone against the batch, and the batch reversed."""
+    g = torch.Generator().manual_seed(hq * 100 + hkv + bs)
+    lens = [1, 2, 255, 256, 257, 4095, 4096, 4097, 9000] + \
+           [int(x) for x in torch.randint(1, 3000, (23,), generator=g)]
+    announce(f"invariant decode hq={hq} hkv={hkv} bs={bs} B={len(lens)}")
+    t = make_device_decode(lens, hq, hkv, gpu, seed=hq + bs, slack=0.1, block_size=bs)
+
+    def run(rows):
+        from qwen3_engine_from_scratch_amd.kernels.paged_attention import paged_attention_decode_hip
+        r = torch.as_tensor(rows, dtype=torch.long, device=gpu)
+        return paged_attention_decode_hip(t["q"][r], t["k"], t["v"], t["bt"], t["seq_lens"],
+                                          t["row_ids"][r], bs, batch_invariant=True)
+
+    rows = list(range(len(lens)))
+    full = run(rows)
+    torch.cuda.synchronize()
+    ref = gpu_dense_decode_fp32(t["q"], t["k"], t["v"], t["bt"], t["seq_lens"], t["row_ids"], bs)
+    assert_close_attn(full, ref, f"invariant hq={hq} hkv={hkv} bs={bs}")
+    for b in rows:
+        alone = run([b])
+        torch.cuda.synchronize()
+        assert torch.equal(alone[0], full[b]), f"hq={hq} hkv={hkv} bs={bs}: row {b} differs alone"
+    rev = rows[::-1]
+    out = run(rev)
+    torch.cuda.synchronize()
+    assert torch.equal(out, full[rev]), f"hq={hq} hkv={hkv} bs={bs}: reversed batch differs"
