@@ -218,7 +218,7 @@ def read_reference(nbytes, dev, reps=5):
     import torch
 
     buf = torch.ones(nbytes // 8, dtype=torch.int64, device=dev)
-    torch.amax(buf)
+    warm_up(lambda: torch.amax(buf))
     torch.cuda.synchronize()
     start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     start.record()
@@ -253,7 +253,7 @@ def stream_read_reference(nbytes, dev, nontemporal=True, reps=5):
                                                 sink.data_ptr(), stream),
                    "qwen3_hbm_read_reference")
 
-    call()
+    warm_up(call)  # as the decode line: untimed calls until the clocks have ramped
     torch.cuda.synchronize()
     start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     start.record()
@@ -352,6 +352,9 @@ def bench_decode(args, dev, batch_invariant=False):
         paged_attention_decode_hip(t["q"], t["k"], t["v"], t["bt"], t["seq_lens"], t["row_ids"],
                                    16, out=out, workspace=ws, batch_invariant=batch_invariant)
 
+    # untimed calls first, so the clocks have ramped up before the W warm-up
+    # steps and the K timed ones (a cold first process measured 4% low)
+    warm_up(step)
     wall_ms, evt_ms = time_steps(step, args.steps, args.warmup)
     nbytes = decode_bytes(lens, hq, hkv)
     log(f"decode: {evt_ms * 1e3:.1f} us/call (events), {wall_ms * 1e3:.1f} us/step (wall)")
